@@ -1,0 +1,169 @@
+/*
+ * tt_attn.h -- C-ABI of the MI355X (gfx950) TinyTensor runtime and its
+ * scaled dot-product attention kernels.
+ *
+ * Every function returns an int status (TT_OK = 0).  On failure the message
+ * is available from tt_last_error() (thread-local).  No C++ exception crosses
+ * this boundary and no type here is a PyTorch or HIP type: pointers are plain
+ * device addresses obtained from tt_malloc, sizes are int64_t / size_t, and a
+ * stream argument of NULL means the library's own stream (tt_stream()).
+ *
+ * Reference interfaces replaced (csxq0605/pku-aiprogramming, Task3/Tinytensor):
+ *   storage      cudaMalloc / cudaFree / cudaMemcpy / cudaMemset calls inside
+ *                TinyTensor<T> (src/Tinytensor.cu:21,39-40,60-61,77-78,90,
+ *                125,189,213,238,251-252,300,376-378)
+ *   elementwise  the grid-stride kernels of src/TinyTensor_kernels.cu:6-85
+ *                (launched at src/Tinytensor.cu:145,167,281,308,322,336,350,
+ *                393,422,427,443,474,479)
+ *   attention    the composition O = softmax((Q @ K^T) * s + M) @ V of
+ *                optimizer/operators.py:163-164,181-182,234-242,194-199,
+ *                611-612,416-433 (forward) and the gradient rules the autodiff
+ *                driver runs over it (optimizer/autodiff.py:33-61), whose GPU
+ *                row-softmax stage is SoftmaxForward (src/Layers.cu:324-349).
+ *
+ * Tensor layout: contiguous row-major [B, H, L, d] (TinyTensor has no
+ * strides, src/Tinytensor.cu:47-66).  bf16 tensors are uint16_t bit patterns.
+ * LSE is float32 [B, H, Lq], natural log.
+ */
+#ifndef TT_ATTN_H
+#define TT_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  TT_OK = 0,
+  TT_ERR_ARG = 1,         /* invalid argument (shape, null pointer, dtype) */
+  TT_ERR_HIP = 2,         /* a HIP runtime call failed */
+  TT_ERR_UNSUPPORTED = 3, /* valid but not implemented (e.g. head dim 96) */
+  TT_ERR_NOMEM = 4        /* device allocation failed */
+};
+
+/* dtype codes for the generic entry points */
+enum { TT_F32 = 0, TT_F64 = 1, TT_I32 = 2, TT_BF16 = 3 };
+
+/* ---------------------------------------------------------------- runtime */
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* tt_last_error(void);
+/* Library version string. */
+const char* tt_version(void);
+/* Number of visible HIP devices (0 without a GPU; never fails). */
+int tt_device_count(int* n);
+/* Select the device and create the library stream (idempotent). */
+int tt_init(int device);
+/* The library stream as an opaque handle (hipStream_t). */
+void* tt_stream(void);
+
+/* Caching device allocator (hipMalloc-backed).
+ * Replaces cudaMalloc at src/Tinytensor.cu:21,39,60,77,116,252,375.
+ * Blocks are reused by size class; tt_empty_cache() returns them to HIP. */
+int tt_malloc(void** ptr, size_t bytes);
+/* Replaces cudaFree at src/Tinytensor.cu:90,108,239,378.  NULL is a no-op. */
+int tt_free(void* ptr);
+int tt_empty_cache(void);
+/* Bytes currently handed out / held in the cache. */
+int tt_mem_stats(size_t* in_use, size_t* cached);
+
+/* Copies ordered on the library stream.  d2h and h2d return after the copy
+ * completed (the reference's copies are synchronous: src/Tinytensor.cu:40,61,
+ * 213,238,251).  d2d is stream-ordered (src/Tinytensor.cu:78,125,189,377). */
+int tt_memcpy_h2d(void* dst, const void* src, size_t bytes);
+int tt_memcpy_d2h(void* dst, const void* src, size_t bytes);
+int tt_memcpy_d2d(void* dst, const void* src, size_t bytes);
+/* Byte fill (src/Tinytensor.cu:300 cudaMemset). */
+int tt_memset(void* ptr, int value, size_t bytes);
+/* Wait for all work on the library stream. */
+int tt_sync(void);
+
+/* Stream-ordered timing events (hipEvent) for benchmarks. */
+int tt_event_create(void** ev);
+int tt_event_record(void* ev, void* stream);
+int tt_event_elapsed_ms(float* ms, void* start, void* stop);
+int tt_event_destroy(void* ev);
+
+/* ------------------------------------------------------------ elementwise */
+
+/* Elementwise ops of TinyTensor (src/TinyTensor_kernels.cu:6-85).
+ * op codes:
+ *   TT_EW_ADD  c = a + b            cudaAdd        (:6-11)
+ *   TT_EW_SUB  c = a - b            cudaSub        (:13-18)
+ *   TT_EW_FILL c = alpha            cudaOnes/cudaFloatks (:30-35, :51-56)
+ *   TT_EW_NEG  c = -a               cudaNegative   (:37-42)
+ *   TT_EW_SCALE c = a * alpha       cudaMults      (:44-49)
+ *   TT_EW_RELU c = max(a, 0)        Relu_Forward   (:58-63)
+ *   TT_EW_RELU_BWD c = a>0 ? b : 0  Relu_Backward  (:65-70)
+ *   TT_EW_SIGMOID c = 1/(1+e^-a)    Sigmoid_Forward (:72-77)
+ *   TT_EW_SIGMOID_BWD c = s(a)(1-s(a)) b  Sigmoid_Backward (:79-85)
+ *   TT_EW_UNIFORM c ~ U[alpha, beta) from a counter hash of (seed, index)
+ *                                   cudaRandom     (:20-28)
+ * a, b may be NULL where unused; c may alias a.  n is the element count. */
+enum {
+  TT_EW_ADD = 0, TT_EW_SUB = 1, TT_EW_FILL = 2, TT_EW_NEG = 3, TT_EW_SCALE = 4,
+  TT_EW_RELU = 5, TT_EW_RELU_BWD = 6, TT_EW_SIGMOID = 7, TT_EW_SIGMOID_BWD = 8,
+  TT_EW_UNIFORM = 9
+};
+int tt_elementwise(int op, int dtype, void* c, const void* a, const void* b, int64_t n,
+                   double alpha, double beta, uint64_t seed, void* stream);
+
+/* Fill a bf16 / fp32 buffer with scale * N(0,1) samples from a counter-based
+ * generator (SplitMix64 of (seed, index) -> Box-Muller).  Synthetic benchmark
+ * data only; not part of the reference. */
+int tt_fill_normal(int dtype, void* dst, int64_t n, uint64_t seed, float scale, void* stream);
+
+/* ------------------------------------------------------------- attention */
+
+/* Forward: O = softmax(scale * Q K^T + M) V, LSE = rowwise log-sum-exp of the
+ * scaled, masked scores (natural log).  M is the strict upper triangle
+ * (key j > query i, top-left aligned) when causal != 0, else nothing.
+ * q [B,H,Lq,d], k/v [B,H,Lk,d], o [B,H,Lq,d], lse [B,H,Lq] (may be NULL).
+ * d in {32, 64, 128}; causal requires Lq == Lk; Lk >= 1 when Lq >= 1.
+ * Replaces the composition at optimizer/operators.py:163-164 (Q @ K^T),
+ * :234-239 (* s), :194-196 (+ mask), :611-612 (softmax), :416-419 (@ V). */
+int tt_attn_fwd_f32(const float* q, const float* k, const float* v, float* o, float* lse,
+                    int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t d,
+                    float scale, int causal, void* stream);
+int tt_attn_fwd_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o,
+                     float* lse, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t d,
+                     float scale, int causal, void* stream);
+
+/* Backward of the forward above for upstream gradient do_ (same shape as o),
+ * from the saved o and lse:  D = rowsum(dO o O); P recomputed from LSE;
+ * dV = P^T dO; dP = dO V^T; dS = P o (dP - D); dQ = s dS K; dK = s dS^T Q.
+ * Replaces O.backward(dO) (optimizer/operators.py:115-119 -> autodiff.py:33-61)
+ * through MatMul.gradient (:421-429), Transpose.gradient (:338-340),
+ * MulScalar.gradient (:241-242), EWiseDiv.gradient (:296-298),
+ * BroadcastTo/Summation.gradient (:373-380, :400-408), Exp.gradient (:469-470).
+ * Uses a library-owned scratch buffer of B*H*Lq floats (the row sums D). */
+int tt_attn_bwd_f32(const float* q, const float* k, const float* v, const float* o,
+                    const float* lse, const float* do_, float* dq, float* dk, float* dv,
+                    int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t d,
+                    float scale, int causal, void* stream);
+int tt_attn_bwd_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                     const uint16_t* o, const float* lse, const uint16_t* do_,
+                     uint16_t* dq, uint16_t* dk, uint16_t* dv,
+                     int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t d,
+                     float scale, int causal, void* stream);
+
+/* Single-query decode: o = softmax(scale * q K^T) V per (b, h), no mask.
+ * q [B,H,1,d], k/v cache [B,H,Lkv,d] contiguous, o [B,H,1,d], lse [B,H] (may
+ * be NULL).  The same composition as the forward with Lq = 1 (a3 -> a4 -> a6
+ * -> a7 of the reference's op chain).  Splits Lkv across workgroups and merges
+ * the partial (o, lse) pairs by LSE rescaling; partials live in a
+ * library-owned scratch buffer. */
+int tt_attn_decode_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o,
+                        float* lse, int64_t B, int64_t H, int64_t Lkv, int64_t d,
+                        float scale, void* stream);
+int tt_attn_decode_f32(const float* q, const float* k, const float* v, float* o, float* lse,
+                       int64_t B, int64_t H, int64_t Lkv, int64_t d, float scale,
+                       void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TT_ATTN_H */

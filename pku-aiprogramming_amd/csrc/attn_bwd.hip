@@ -1,0 +1,662 @@
+// Fused attention backward for gfx950.
+//
+// Replaces O.backward(dO) over the reference's composition
+// (optimizer/operators.py:115-119 -> autodiff.py:33-61) through the gradient
+// rules MatMul (:421-429), Transpose (:338-340), MulScalar (:241-242),
+// EWiseDiv (:296-298), BroadcastTo (:373-380), Summation (:400-408) and
+// Exp (:469-470).  Closed form of that chain, with P recomputed from the LSE
+// saved by the forward so no L x L tensor is ever stored:
+//   D_i  = sum_d dO_id O_id                  (pre-pass, fp32 [B,H,L])
+//   P    = exp(s Q K^T + M - LSE)
+//   dV   = P^T dO,   dP = dO V^T,   dS = P o (dP - D)
+//   dQ   = s dS K,   dK = s dS^T Q
+//
+// Two kernels split the work so that every output row has one owner and no
+// atomics are needed:
+//   dkdv: workgroup = 128 keys (32 per wave, lane = key); loops over query
+//         tiles of 64 staged in LDS both row-major (S, dP operands) and
+//         transposed (dV^T += dO^T P, dK^T += Q^T dS operands).
+//   dq:   workgroup = 128 queries (lane = query, as in the forward); loops over
+//         key tiles of 64 staged row-major (S^T, dP^T) and transposed
+//         (dQ^T += K^T dS^T).
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+
+#include "attn_common.h"
+#include "attn_tiles.h"
+
+namespace tt {
+
+constexpr int DKDV_BN = 128;  // keys per workgroup
+constexpr int DKDV_BQ = 64;   // queries per LDS step
+constexpr int DQ_BM = 128;    // queries per workgroup
+constexpr int DQ_BN = 64;     // keys per LDS step
+
+// D_i = sum_d dO[i][d] * O[i][d], one 16-byte chunk per thread.
+template <typename T, int D>
+__global__ __launch_bounds__(256) void attn_bwd_delta_kernel(const T* __restrict__ O,
+                                                             const T* __restrict__ dO,
+                                                             float* __restrict__ Delta, int64_t rows) {
+  constexpr int EPT = 16 / sizeof(T);
+  constexpr int TPR = D / EPT;  // threads per row (a power of two <= 32)
+  constexpr int RPB = 256 / TPR;
+  const int64_t row = (int64_t)blockIdx.x * RPB + threadIdx.x / TPR;
+  const int col = threadIdx.x % TPR;
+  float sum = 0.f;
+  if (row < rows) {
+    uint4 a = ldg16(O + row * D + col * EPT);
+    uint4 b = ldg16(dO + row * D + col * EPT);
+    if constexpr (sizeof(T) == 2) {
+      const u16* pa = reinterpret_cast<const u16*>(&a);
+      const u16* pb = reinterpret_cast<const u16*>(&b);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sum += bf16_to_f32(pa[e]) * bf16_to_f32(pb[e]);
+    } else {
+      const float* pa = reinterpret_cast<const float*>(&a);
+      const float* pb = reinterpret_cast<const float*>(&b);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sum += pa[e] * pb[e];
+    }
+  }
+#pragma unroll
+  for (int off = TPR / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+  if (col == 0 && row < rows) Delta[row] = sum;
+}
+
+// ------------------------------------------------------------------ bf16 dK, dV
+template <int D, bool CAUSAL>
+__global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_bf16_kernel(
+    const u16* __restrict__ Q, const u16* __restrict__ K, const u16* __restrict__ V,
+    const u16* __restrict__ dO, const float* __restrict__ LSE, const float* __restrict__ Delta,
+    u16* __restrict__ dK, u16* __restrict__ dV, int Lq, int Lk, int BH, int nkt, int group, float sl2,
+    float scale) {
+  constexpr int BN = DKDV_BN, BQ = DKDV_BQ;
+  constexpr int RP = D + 8;   // row-major pitch
+  constexpr int TP = BQ + 8;  // transposed pitch
+  constexpr int NC = D / 16, ND = D / 32, CPR = D / 8;
+  constexpr int LPT = BQ * CPR / 256;
+  __shared__ __align__(16) u16 sQ[BQ * RP];
+  __shared__ __align__(16) u16 sdO[BQ * RP];
+  __shared__ __align__(16) u16 sQt[D * TP];
+  __shared__ __align__(16) u16 sdOt[D * TP];
+  __shared__ __align__(16) float sL[BQ];
+  __shared__ __align__(16) float sDl[BQ];
+
+  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, g = l >> 5, r32 = l & 31;
+  int kt, bh;
+  map_tile(blockIdx.x, nkt, BH, group, kt, bh, false);  // causal: key tile 0 sees every query
+  const int k0 = kt * BN;
+  const int key = k0 + 32 * w + r32;
+  const int wk_lo = k0 + 32 * w;
+  const int64_t qbase = (int64_t)bh * Lq * D;
+  const int64_t kbase = (int64_t)bh * Lk * D;
+  const int64_t lbase = (int64_t)bh * Lq;
+
+  bf16x8 kf[NC], vf[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    uint4 a = {0, 0, 0, 0}, b = {0, 0, 0, 0};
+    if (key < Lk) {
+      a = ldg16(K + kbase + (int64_t)key * D + 16 * c + 8 * g);
+      b = ldg16(V + kbase + (int64_t)key * D + 16 * c + 8 * g);
+    }
+    kf[c] = *reinterpret_cast<bf16x8*>(&a);
+    vf[c] = *reinterpret_cast<bf16x8*>(&b);
+  }
+  f32x16 adk[ND], adv[ND];
+#pragma unroll
+  for (int dt = 0; dt < ND; ++dt) adk[dt] = adv[dt] = f32x16{};
+
+  uint4 qreg[LPT], oreg[LPT];
+  float lreg = 0.f, dreg = 0.f;
+  auto gload = [&](int qb) {
+#pragma unroll
+    for (int i = 0; i < LPT; ++i) {
+      const int c = tid + 256 * i;
+      const int row = c % BQ, ch = c / BQ;  // row-fastest: conflict-free transposed stores
+      uint4 z = {0, 0, 0, 0};
+      const bool in = qb + row < Lq;
+      qreg[i] = in ? ldg16(Q + qbase + (int64_t)(qb + row) * D + 8 * ch) : z;
+      oreg[i] = in ? ldg16(dO + qbase + (int64_t)(qb + row) * D + 8 * ch) : z;
+    }
+    if (tid < BQ) {
+      const bool in = qb + tid < Lq;
+      lreg = in ? LSE[lbase + qb + tid] * kLog2e : INFINITY;  // +inf -> P = 0 for padding rows
+      dreg = in ? Delta[lbase + qb + tid] : 0.f;
+    }
+  };
+  auto sstore = [&]() {
+#pragma unroll
+    for (int i = 0; i < LPT; ++i) {
+      const int c = tid + 256 * i;
+      const int row = c % BQ, ch = c / BQ;
+      *reinterpret_cast<uint4*>(&sQ[row * RP + 8 * ch]) = qreg[i];
+      *reinterpret_cast<uint4*>(&sdO[row * RP + 8 * ch]) = oreg[i];
+      const u16* eq = reinterpret_cast<const u16*>(&qreg[i]);
+      const u16* eo = reinterpret_cast<const u16*>(&oreg[i]);
+      const int pos = perm16(row);
+#pragma unroll
+      for (int x = 0; x < 8; ++x) {
+        sQt[(8 * ch + x) * TP + pos] = eq[x];
+        sdOt[(8 * ch + x) * TP + pos] = eo[x];
+      }
+    }
+    if (tid < BQ) {
+      sL[tid] = lreg;
+      sDl[tid] = dreg;
+    }
+  };
+
+  const int qstart = CAUSAL ? (k0 / BQ) * BQ : 0;
+  if (qstart < Lq) gload(qstart);
+  for (int qb = qstart; qb < Lq; qb += BQ) {
+    __syncthreads();
+    sstore();
+    __syncthreads();
+    if (qb + BQ < Lq) gload(qb + BQ);
+    if (CAUSAL && qb + BQ - 1 < wk_lo) continue;  // every query of the tile precedes every key of the wave
+
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      f32x16 s = f32x16{}, dp = f32x16{};
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        bf16x8 a = *reinterpret_cast<const bf16x8*>(&sQ[(32 * mt + r32) * RP + 16 * c + 8 * g]);
+        s = mfma_bf16_32x32x16(a, kf[c], s);
+      }
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        bf16x8 a = *reinterpret_cast<const bf16x8*>(&sdO[(32 * mt + r32) * RP + 16 * c + 8 * g]);
+        dp = mfma_bf16_32x32x16(a, vf[c], dp);
+      }
+      // s[r] = S[query qb + 32mt + acc_row(r, g)][key]
+      const bool need_mask = CAUSAL && (qb + 32 * mt < wk_lo + 31);
+      bf16x8 pb[2], db[2];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int qi = 32 * mt + 8 * j + 4 * g;  // rows acc_row(4j..4j+3, g)
+        const float4 lv = *reinterpret_cast<const float4*>(&sL[qi]);
+        const float4 dv = *reinterpret_cast<const float4*>(&sDl[qi]);
+        const float la[4] = {lv.x, lv.y, lv.z, lv.w};
+        const float da[4] = {dv.x, dv.y, dv.z, dv.w};
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int r = 4 * j + u;
+          float p = fast_exp2(s[r] * sl2 - la[u]);
+          if (need_mask && key > qb + qi + u) p = 0.f;
+          const float ds = p * (dp[r] - da[u]);
+          pb[r >> 3][r & 7] = (__bf16)p;
+          db[r >> 3][r & 7] = (__bf16)ds;
+        }
+      }
+#pragma unroll
+      for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int off = (32 * dt + r32) * TP + 16 * (2 * mt + h) + 8 * g;
+          bf16x8 ao = *reinterpret_cast<const bf16x8*>(&sdOt[off]);
+          adv[dt] = mfma_bf16_32x32x16(ao, pb[h], adv[dt]);
+          bf16x8 aq = *reinterpret_cast<const bf16x8*>(&sQt[off]);
+          adk[dt] = mfma_bf16_32x32x16(aq, db[h], adk[dt]);
+        }
+    }
+  }
+
+  if (key < Lk) {
+    u16* dkrow = dK + kbase + (int64_t)key * D;
+    u16* dvrow = dV + kbase + (int64_t)key * D;
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; r += 4) {
+        const int d0 = 32 * dt + acc_row(r, g);
+        uint2 a, b;
+        a.x = pack_bf16x2(adk[dt][r] * scale, adk[dt][r + 1] * scale);
+        a.y = pack_bf16x2(adk[dt][r + 2] * scale, adk[dt][r + 3] * scale);
+        b.x = pack_bf16x2(adv[dt][r], adv[dt][r + 1]);
+        b.y = pack_bf16x2(adv[dt][r + 2], adv[dt][r + 3]);
+        *reinterpret_cast<uint2*>(dkrow + d0) = a;
+        *reinterpret_cast<uint2*>(dvrow + d0) = b;
+      }
+  }
+}
+
+// ------------------------------------------------------------------ bf16 dQ
+template <int D, bool CAUSAL>
+__global__ __launch_bounds__(256, 1) void attn_bwd_dq_bf16_kernel(
+    const u16* __restrict__ Q, const u16* __restrict__ K, const u16* __restrict__ V,
+    const u16* __restrict__ dO, const float* __restrict__ LSE, const float* __restrict__ Delta,
+    u16* __restrict__ dQ, int Lq, int Lk, int BH, int nqt, int group, float sl2, float scale) {
+  constexpr int BM = DQ_BM, BN = DQ_BN;
+  constexpr int RP = D + 8, TP = BN + 8;
+  constexpr int NC = D / 16, ND = D / 32, CPR = D / 8;
+  constexpr int LPT = BN * CPR / 256;
+  __shared__ __align__(16) u16 sK[BN * RP];
+  __shared__ __align__(16) u16 sV[BN * RP];
+  __shared__ __align__(16) u16 sKt[D * TP];
+
+  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, g = l >> 5, r32 = l & 31;
+  int qt, bh;
+  map_tile(blockIdx.x, nqt, BH, group, qt, bh, CAUSAL);
+  const int q0 = qt * BM;
+  const int qrow = q0 + 32 * w + r32;
+  const int wq_lo = q0 + 32 * w, wq_hi = wq_lo + 31;
+  const int64_t qbase = (int64_t)bh * Lq * D;
+  const int64_t kbase = (int64_t)bh * Lk * D;
+
+  bf16x8 qf[NC], dof[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    uint4 a = {0, 0, 0, 0}, b = {0, 0, 0, 0};
+    if (qrow < Lq) {
+      a = ldg16(Q + qbase + (int64_t)qrow * D + 16 * c + 8 * g);
+      b = ldg16(dO + qbase + (int64_t)qrow * D + 16 * c + 8 * g);
+    }
+    qf[c] = *reinterpret_cast<bf16x8*>(&a);
+    dof[c] = *reinterpret_cast<bf16x8*>(&b);
+  }
+  const float lse2 = qrow < Lq ? LSE[(int64_t)bh * Lq + qrow] * kLog2e : INFINITY;
+  const float dl = qrow < Lq ? Delta[(int64_t)bh * Lq + qrow] : 0.f;
+  f32x16 adq[ND];
+#pragma unroll
+  for (int dt = 0; dt < ND; ++dt) adq[dt] = f32x16{};
+
+  uint4 kreg[LPT], vreg[LPT];
+  auto gload = [&](int kb) {
+#pragma unroll
+    for (int i = 0; i < LPT; ++i) {
+      const int c = tid + 256 * i;
+      const int key = c % BN, ch = c / BN;
+      uint4 z = {0, 0, 0, 0};
+      const bool in = kb + key < Lk;
+      kreg[i] = in ? ldg16(K + kbase + (int64_t)(kb + key) * D + 8 * ch) : z;
+      vreg[i] = in ? ldg16(V + kbase + (int64_t)(kb + key) * D + 8 * ch) : z;
+    }
+  };
+  auto sstore = [&]() {
+#pragma unroll
+    for (int i = 0; i < LPT; ++i) {
+      const int c = tid + 256 * i;
+      const int key = c % BN, ch = c / BN;
+      *reinterpret_cast<uint4*>(&sK[key * RP + 8 * ch]) = kreg[i];
+      *reinterpret_cast<uint4*>(&sV[key * RP + 8 * ch]) = vreg[i];
+      const u16* ek = reinterpret_cast<const u16*>(&kreg[i]);
+      const int pos = perm16(key);
+#pragma unroll
+      for (int x = 0; x < 8; ++x) sKt[(8 * ch + x) * TP + pos] = ek[x];
+    }
+  };
+
+  const int kend = CAUSAL ? min(Lk, q0 + BM) : Lk;
+  if (kend > 0) gload(0);
+  for (int kb = 0; kb < kend; kb += BN) {
+    __syncthreads();
+    sstore();
+    __syncthreads();
+    if (kb + BN < kend) gload(kb + BN);
+    if (CAUSAL && kb > wq_hi) continue;
+    const bool need_mask = (kb + BN > Lk) || (CAUSAL && kb + BN - 1 > wq_lo);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      f32x16 s = f32x16{}, dp = f32x16{};
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        bf16x8 a = *reinterpret_cast<const bf16x8*>(&sK[(32 * t + r32) * RP + 16 * c + 8 * g]);
+        s = mfma_bf16_32x32x16(a, qf[c], s);
+      }
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        bf16x8 a = *reinterpret_cast<const bf16x8*>(&sV[(32 * t + r32) * RP + 16 * c + 8 * g]);
+        dp = mfma_bf16_32x32x16(a, dof[c], dp);
+      }
+      bf16x8 db[2];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float p = fast_exp2(s[r] * sl2 - lse2);
+        if (need_mask) {
+          const int kk = kb + 32 * t + acc_row(r, g);
+          if (kk >= Lk || (CAUSAL && kk > qrow)) p = 0.f;
+        }
+        db[r >> 3][r & 7] = (__bf16)(p * (dp[r] - dl));
+      }
+#pragma unroll
+      for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          bf16x8 a = *reinterpret_cast<const bf16x8*>(&sKt[(32 * dt + r32) * TP + 16 * (2 * t + h) + 8 * g]);
+          adq[dt] = mfma_bf16_32x32x16(a, db[h], adq[dt]);
+        }
+    }
+  }
+
+  if (qrow < Lq) {
+    u16* row = dQ + qbase + (int64_t)qrow * D;
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; r += 4) {
+        uint2 v;
+        v.x = pack_bf16x2(adq[dt][r] * scale, adq[dt][r + 1] * scale);
+        v.y = pack_bf16x2(adq[dt][r + 2] * scale, adq[dt][r + 3] * scale);
+        *reinterpret_cast<uint2*>(row + 32 * dt + acc_row(r, g)) = v;
+      }
+  }
+}
+
+// ------------------------------------------------------------------ fp32 dK, dV
+template <int D, bool CAUSAL>
+__global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_f32_kernel(
+    const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
+    const float* __restrict__ dO, const float* __restrict__ LSE, const float* __restrict__ Delta,
+    float* __restrict__ dK, float* __restrict__ dV, int Lq, int Lk, int BH, int nkt, int group,
+    float sl2, float scale) {
+  constexpr int BN = DKDV_BN, BQ = DKDV_BQ;
+  constexpr int P = D + 1;
+  constexpr int NC = D / 2, ND = D / 32, CPR = D / 4;
+  constexpr int LPT = BQ * CPR / 256;
+  __shared__ float sQ[BQ * P];
+  __shared__ float sdO[BQ * P];
+  __shared__ float sL[BQ];
+  __shared__ float sDl[BQ];
+
+  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, g = l >> 5, r32 = l & 31;
+  int kt, bh;
+  map_tile(blockIdx.x, nkt, BH, group, kt, bh, false);
+  const int k0 = kt * BN;
+  const int key = k0 + 32 * w + r32;
+  const int wk_lo = k0 + 32 * w;
+  const int64_t qbase = (int64_t)bh * Lq * D;
+  const int64_t kbase = (int64_t)bh * Lk * D;
+  const int64_t lbase = (int64_t)bh * Lq;
+
+  float kf[NC], vf[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    kf[c] = key < Lk ? K[kbase + (int64_t)key * D + 2 * c + g] : 0.f;
+    vf[c] = key < Lk ? V[kbase + (int64_t)key * D + 2 * c + g] : 0.f;
+  }
+  f32x16 adk[ND], adv[ND];
+#pragma unroll
+  for (int dt = 0; dt < ND; ++dt) adk[dt] = adv[dt] = f32x16{};
+
+  float4 qreg[LPT], oreg[LPT];
+  float lreg = 0.f, dreg = 0.f;
+  auto gload = [&](int qb) {
+#pragma unroll
+    for (int i = 0; i < LPT; ++i) {
+      const int c = tid + 256 * i;
+      const int row = c / CPR, ch = c % CPR;
+      float4 z = {0.f, 0.f, 0.f, 0.f};
+      const bool in = qb + row < Lq;
+      qreg[i] = in ? *reinterpret_cast<const float4*>(Q + qbase + (int64_t)(qb + row) * D + 4 * ch) : z;
+      oreg[i] = in ? *reinterpret_cast<const float4*>(dO + qbase + (int64_t)(qb + row) * D + 4 * ch) : z;
+    }
+    if (tid < BQ) {
+      const bool in = qb + tid < Lq;
+      lreg = in ? LSE[lbase + qb + tid] * kLog2e : INFINITY;
+      dreg = in ? Delta[lbase + qb + tid] : 0.f;
+    }
+  };
+  auto sstore = [&]() {
+#pragma unroll
+    for (int i = 0; i < LPT; ++i) {
+      const int c = tid + 256 * i;
+      const int row = c / CPR, ch = c % CPR;
+      float* pq = &sQ[row * P + 4 * ch];
+      float* po = &sdO[row * P + 4 * ch];
+      pq[0] = qreg[i].x; pq[1] = qreg[i].y; pq[2] = qreg[i].z; pq[3] = qreg[i].w;
+      po[0] = oreg[i].x; po[1] = oreg[i].y; po[2] = oreg[i].z; po[3] = oreg[i].w;
+    }
+    if (tid < BQ) {
+      sL[tid] = lreg;
+      sDl[tid] = dreg;
+    }
+  };
+
+  const int qstart = CAUSAL ? (k0 / BQ) * BQ : 0;
+  if (qstart < Lq) gload(qstart);
+  for (int qb = qstart; qb < Lq; qb += BQ) {
+    __syncthreads();
+    sstore();
+    __syncthreads();
+    if (qb + BQ < Lq) gload(qb + BQ);
+    if (CAUSAL && qb + BQ - 1 < wk_lo) continue;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      f32x16 s = f32x16{}, dp = f32x16{};
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        s = mfma_f32_32x32x2(sQ[(32 * mt + r32) * P + 2 * c + g], kf[c], s);
+        dp = mfma_f32_32x32x2(sdO[(32 * mt + r32) * P + 2 * c + g], vf[c], dp);
+      }
+      const bool need_mask = CAUSAL && (qb + 32 * mt < wk_lo + 31);
+      float pr[16], dsr[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int qi = 32 * mt + acc_row(r, g);
+        float p = fast_exp2(s[r] * sl2 - sL[qi]);
+        if (need_mask && key > qb + qi) p = 0.f;
+        pr[r] = p;
+        dsr[r] = p * (dp[r] - sDl[qi]);
+      }
+#pragma unroll
+      for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int qi = 32 * mt + acc_row(r, g);
+          adv[dt] = mfma_f32_32x32x2(sdO[qi * P + 32 * dt + r32], pr[r], adv[dt]);
+          adk[dt] = mfma_f32_32x32x2(sQ[qi * P + 32 * dt + r32], dsr[r], adk[dt]);
+        }
+    }
+  }
+
+  if (key < Lk) {
+    float* dkrow = dK + kbase + (int64_t)key * D;
+    float* dvrow = dV + kbase + (int64_t)key * D;
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; r += 4) {
+        const int d0 = 32 * dt + acc_row(r, g);
+        float4 a = {adk[dt][r] * scale, adk[dt][r + 1] * scale, adk[dt][r + 2] * scale, adk[dt][r + 3] * scale};
+        float4 b = {adv[dt][r], adv[dt][r + 1], adv[dt][r + 2], adv[dt][r + 3]};
+        *reinterpret_cast<float4*>(dkrow + d0) = a;
+        *reinterpret_cast<float4*>(dvrow + d0) = b;
+      }
+  }
+}
+
+// ------------------------------------------------------------------ fp32 dQ
+template <int D, bool CAUSAL>
+__global__ __launch_bounds__(256, 1) void attn_bwd_dq_f32_kernel(
+    const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
+    const float* __restrict__ dO, const float* __restrict__ LSE, const float* __restrict__ Delta,
+    float* __restrict__ dQ, int Lq, int Lk, int BH, int nqt, int group, float sl2, float scale) {
+  constexpr int BM = DQ_BM, BN = DQ_BN;
+  constexpr int P = D + 1;
+  constexpr int NC = D / 2, ND = D / 32, CPR = D / 4;
+  constexpr int LPT = BN * CPR / 256;
+  __shared__ float sK[BN * P];
+  __shared__ float sV[BN * P];
+
+  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, g = l >> 5, r32 = l & 31;
+  int qt, bh;
+  map_tile(blockIdx.x, nqt, BH, group, qt, bh, CAUSAL);
+  const int q0 = qt * BM;
+  const int qrow = q0 + 32 * w + r32;
+  const int wq_lo = q0 + 32 * w, wq_hi = wq_lo + 31;
+  const int64_t qbase = (int64_t)bh * Lq * D;
+  const int64_t kbase = (int64_t)bh * Lk * D;
+
+  float qf[NC], dof[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    qf[c] = qrow < Lq ? Q[qbase + (int64_t)qrow * D + 2 * c + g] : 0.f;
+    dof[c] = qrow < Lq ? dO[qbase + (int64_t)qrow * D + 2 * c + g] : 0.f;
+  }
+  const float lse2 = qrow < Lq ? LSE[(int64_t)bh * Lq + qrow] * kLog2e : INFINITY;
+  const float dl = qrow < Lq ? Delta[(int64_t)bh * Lq + qrow] : 0.f;
+  f32x16 adq[ND];
+#pragma unroll
+  for (int dt = 0; dt < ND; ++dt) adq[dt] = f32x16{};
+
+  float4 kreg[LPT], vreg[LPT];
+  auto gload = [&](int kb) {
+#pragma unroll
+    for (int i = 0; i < LPT; ++i) {
+      const int c = tid + 256 * i;
+      const int key = c / CPR, ch = c % CPR;
+      float4 z = {0.f, 0.f, 0.f, 0.f};
+      const bool in = kb + key < Lk;
+      kreg[i] = in ? *reinterpret_cast<const float4*>(K + kbase + (int64_t)(kb + key) * D + 4 * ch) : z;
+      vreg[i] = in ? *reinterpret_cast<const float4*>(V + kbase + (int64_t)(kb + key) * D + 4 * ch) : z;
+    }
+  };
+  auto sstore = [&]() {
+#pragma unroll
+    for (int i = 0; i < LPT; ++i) {
+      const int c = tid + 256 * i;
+      const int key = c / CPR, ch = c % CPR;
+      float* pk = &sK[key * P + 4 * ch];
+      float* pv = &sV[key * P + 4 * ch];
+      pk[0] = kreg[i].x; pk[1] = kreg[i].y; pk[2] = kreg[i].z; pk[3] = kreg[i].w;
+      pv[0] = vreg[i].x; pv[1] = vreg[i].y; pv[2] = vreg[i].z; pv[3] = vreg[i].w;
+    }
+  };
+
+  const int kend = CAUSAL ? min(Lk, q0 + BM) : Lk;
+  if (kend > 0) gload(0);
+  for (int kb = 0; kb < kend; kb += BN) {
+    __syncthreads();
+    sstore();
+    __syncthreads();
+    if (kb + BN < kend) gload(kb + BN);
+    if (CAUSAL && kb > wq_hi) continue;
+    const bool need_mask = (kb + BN > Lk) || (CAUSAL && kb + BN - 1 > wq_lo);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      f32x16 s = f32x16{}, dp = f32x16{};
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        s = mfma_f32_32x32x2(sK[(32 * t + r32) * P + 2 * c + g], qf[c], s);
+        dp = mfma_f32_32x32x2(sV[(32 * t + r32) * P + 2 * c + g], dof[c], dp);
+      }
+      float dsr[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float p = fast_exp2(s[r] * sl2 - lse2);
+        if (need_mask) {
+          const int kk = kb + 32 * t + acc_row(r, g);
+          if (kk >= Lk || (CAUSAL && kk > qrow)) p = 0.f;
+        }
+        dsr[r] = p * (dp[r] - dl);
+      }
+#pragma unroll
+      for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          adq[dt] = mfma_f32_32x32x2(sK[(32 * t + acc_row(r, g)) * P + 32 * dt + r32], dsr[r], adq[dt]);
+    }
+  }
+
+  if (qrow < Lq) {
+    float* row = dQ + qbase + (int64_t)qrow * D;
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; r += 4) {
+        float4 v = {adq[dt][r] * scale, adq[dt][r + 1] * scale, adq[dt][r + 2] * scale, adq[dt][r + 3] * scale};
+        *reinterpret_cast<float4*>(row + 32 * dt + acc_row(r, g)) = v;
+      }
+  }
+}
+
+// ------------------------------------------------------------------ launchers
+template <typename T, int D, bool CAUSAL>
+static int launch_bwd(const T* q, const T* k, const T* v, const T* o, const float* lse, const T* dout,
+                      T* dq, T* dk, T* dv, int64_t BH, int64_t Lq, int64_t Lk, float scale, hipStream_t st) {
+  constexpr bool BF = sizeof(T) == 2;
+  float* delta = nullptr;
+  int rc = workspace(0, (size_t)(BH * Lq) * sizeof(float), (void**)&delta);
+  if (rc) return rc;
+  const int64_t rows = BH * Lq;
+  constexpr int TPR = D / (16 / (int)sizeof(T));
+  const int64_t dblk = (rows + (256 / TPR) - 1) / (256 / TPR);
+  if (dblk > 0x7fffffff) return fail(TT_ERR_ARG, "attention backward: grid too large");
+  hipLaunchKernelGGL((attn_bwd_delta_kernel<T, D>), dim3((unsigned)dblk), dim3(256), 0, st, o, dout, delta, rows);
+  TT_LAUNCH_CHECK("attention backward delta launch");
+
+  const float sl2 = scale * kLog2e;
+  const int64_t nkt = (Lk + DKDV_BN - 1) / DKDV_BN;
+  const int64_t nqt = (Lq + DQ_BM - 1) / DQ_BM;
+  if (nkt * BH > 0x7fffffff || nqt * BH > 0x7fffffff) return fail(TT_ERR_ARG, "attention backward: grid too large");
+  const int gk = pick_group(BH, nkt, 32), gq = pick_group(BH, nqt, 32);
+  if constexpr (BF) {
+    hipLaunchKernelGGL((attn_bwd_dkdv_bf16_kernel<D, CAUSAL>), dim3((unsigned)(nkt * BH)), dim3(256), 0, st,
+                       q, k, v, dout, lse, delta, dk, dv, (int)Lq, (int)Lk, (int)BH, (int)nkt, gk, sl2, scale);
+    TT_LAUNCH_CHECK("attention backward dK/dV launch");
+    hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<D, CAUSAL>), dim3((unsigned)(nqt * BH)), dim3(256), 0, st,
+                       q, k, v, dout, lse, delta, dq, (int)Lq, (int)Lk, (int)BH, (int)nqt, gq, sl2, scale);
+    TT_LAUNCH_CHECK("attention backward dQ launch");
+  } else {
+    hipLaunchKernelGGL((attn_bwd_dkdv_f32_kernel<D, CAUSAL>), dim3((unsigned)(nkt * BH)), dim3(256), 0, st,
+                       q, k, v, dout, lse, delta, dk, dv, (int)Lq, (int)Lk, (int)BH, (int)nkt, gk, sl2, scale);
+    TT_LAUNCH_CHECK("attention backward dK/dV launch");
+    hipLaunchKernelGGL((attn_bwd_dq_f32_kernel<D, CAUSAL>), dim3((unsigned)(nqt * BH)), dim3(256), 0, st,
+                       q, k, v, dout, lse, delta, dq, (int)Lq, (int)Lk, (int)BH, (int)nqt, gq, sl2, scale);
+    TT_LAUNCH_CHECK("attention backward dQ launch");
+  }
+  return ok();
+}
+
+template <typename T>
+static int bwd_entry(const char* fn, const T* q, const T* k, const T* v, const T* o, const float* lse,
+                     const T* dout, T* dq, T* dk, T* dv, int64_t B, int64_t H, int64_t Lq, int64_t Lk,
+                     int64_t d, float scale, int causal, void* stream) {
+  int rc = check_attn_shape(fn, B, H, Lq, Lk, d, causal);
+  if (rc) return rc;
+  const int64_t BH = B * H;
+  if (BH == 0) return ok();
+  if ((rc = ensure_init())) return rc;
+  hipStream_t st = stream_or_default(stream);
+  if (Lq == 0) {  // no queries: every key gets zero gradient
+    if (Lk > 0) {
+      if (!dk || !dv) return fail(TT_ERR_ARG, std::string(fn) + ": null pointer");
+      TT_HIP(hipMemsetAsync(dk, 0, (size_t)(BH * Lk * d) * sizeof(T), st));
+      TT_HIP(hipMemsetAsync(dv, 0, (size_t)(BH * Lk * d) * sizeof(T), st));
+    }
+    return ok();
+  }
+  if (!q || !k || !v || !o || !lse || !dout || !dq || !dk || !dv)
+    return fail(TT_ERR_ARG, std::string(fn) + ": null pointer");
+  switch (d * 2 + (causal ? 1 : 0)) {
+    case 64: return launch_bwd<T, 32, false>(q, k, v, o, lse, dout, dq, dk, dv, BH, Lq, Lk, scale, st);
+    case 65: return launch_bwd<T, 32, true>(q, k, v, o, lse, dout, dq, dk, dv, BH, Lq, Lk, scale, st);
+    case 128: return launch_bwd<T, 64, false>(q, k, v, o, lse, dout, dq, dk, dv, BH, Lq, Lk, scale, st);
+    case 129: return launch_bwd<T, 64, true>(q, k, v, o, lse, dout, dq, dk, dv, BH, Lq, Lk, scale, st);
+    case 256: return launch_bwd<T, 128, false>(q, k, v, o, lse, dout, dq, dk, dv, BH, Lq, Lk, scale, st);
+    case 257: return launch_bwd<T, 128, true>(q, k, v, o, lse, dout, dq, dk, dv, BH, Lq, Lk, scale, st);
+    default: return fail(TT_ERR_UNSUPPORTED, std::string(fn) + ": unsupported head dim");
+  }
+}
+
+}  // namespace tt
+
+using namespace tt;
+
+extern "C" int tt_attn_bwd_f32(const float* q, const float* k, const float* v, const float* o,
+                               const float* lse, const float* do_, float* dq, float* dk, float* dv,
+                               int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t d, float scale,
+                               int causal, void* stream) {
+  return bwd_entry<float>("tt_attn_bwd_f32", q, k, v, o, lse, do_, dq, dk, dv, B, H, Lq, Lk, d, scale,
+                          causal, stream);
+}
+
+extern "C" int tt_attn_bwd_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                const uint16_t* o, const float* lse, const uint16_t* do_, uint16_t* dq,
+                                uint16_t* dk, uint16_t* dv, int64_t B, int64_t H, int64_t Lq, int64_t Lk,
+                                int64_t d, float scale, int causal, void* stream) {
+  return bwd_entry<u16>("tt_attn_bwd_bf16", q, k, v, o, lse, do_, dq, dk, dv, B, H, Lq, Lk, d, scale,
+                        causal, stream);
+}

@@ -1,0 +1,362 @@
+// Fused attention forward for gfx950:  O = softmax(s Q K^T + M) V, LSE.
+//
+// Replaces the reference's op chain Q @ K^T -> * s -> + mask -> softmax -> @ V
+// (optimizer/operators.py:163-164, 234-239, 194-196, 611-612, 416-419; GPU
+// softmax order max -> sub -> exp -> sum -> div of src/Layers.cu:324-349)
+// with one kernel that never writes the L x L score matrix.
+//
+// Workgroup = 4 wavefronts = 128 queries of one (b, h); wave w owns queries
+// q0 + 32w .. q0 + 32w + 31, one per lane column.  K/V stream through LDS in
+// tiles of 64 keys; the next tile's global loads are issued before the MFMAs
+// of the current one.  Per tile and wave:
+//   S^T (64 keys x 32 queries) = K Q^T     (bf16 MFMA, Q held in registers)
+//   online softmax in the log2 domain      (running max m, running sum l)
+//   O^T (d x 32 queries) += V^T P^T        (P rounded to bf16, fp32 accum.)
+// The fp32 variant runs the same schedule on v_mfma_f32_32x32x2f32 with P kept
+// in fp32, which keeps the fp32 configs inside 1e-4.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+
+#include "attn_common.h"
+#include "attn_tiles.h"
+
+namespace tt {
+
+constexpr int FWD_BM = 128;  // queries per workgroup
+constexpr int FWD_BN = 64;   // keys per LDS tile
+
+template <int D, bool CAUSAL>
+__global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(
+    const u16* __restrict__ Q, const u16* __restrict__ K, const u16* __restrict__ V,
+    u16* __restrict__ O, float* __restrict__ LSE, int Lq, int Lk, int BH, int nqt, int group,
+    float sl2) {
+  constexpr int BM = FWD_BM, BN = FWD_BN;
+  constexpr int KP = D + 8;   // sK row pitch (elements): 16-byte aligned, rows shift 4 banks
+  constexpr int VP = BN + 8;  // sVt row pitch
+  constexpr int NC = D / 16;  // 16-wide k-chunks of the d contraction
+  constexpr int ND = D / 32;  // 32-row tiles of O^T
+  constexpr int CPR = D / 8;  // 16-byte chunks per row
+  constexpr int LPT = BN * CPR / 256;  // chunks per thread per tile
+  __shared__ __align__(16) u16 sK[BN * KP];
+  __shared__ __align__(16) u16 sVt[D * VP];
+
+  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, g = l >> 5, r32 = l & 31;
+  int qt, bh;
+  map_tile(blockIdx.x, nqt, BH, group, qt, bh, CAUSAL);
+  const int q0 = qt * BM;
+  const int qrow = q0 + 32 * w + r32;
+  const int64_t qbase = (int64_t)bh * Lq * D;
+  const int64_t kbase = (int64_t)bh * Lk * D;
+
+  bf16x8 qf[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    if (qrow < Lq) {
+      uint4 t = ldg16(Q + qbase + (int64_t)qrow * D + 16 * c + 8 * g);
+      qf[c] = *reinterpret_cast<bf16x8*>(&t);
+    } else {
+      uint4 z = {0, 0, 0, 0};
+      qf[c] = *reinterpret_cast<bf16x8*>(&z);
+    }
+  }
+
+  f32x16 acc[ND];
+#pragma unroll
+  for (int dt = 0; dt < ND; ++dt) acc[dt] = f32x16{};
+  float m = -INFINITY, lsum = 0.f;
+
+  const int kend = CAUSAL ? min(Lk, q0 + BM) : Lk;
+  const int wq_lo = q0 + 32 * w, wq_hi = wq_lo + 31;
+
+  uint4 kreg[LPT], vreg[LPT];
+  auto gload = [&](int kb) {
+#pragma unroll
+    for (int i = 0; i < LPT; ++i) {
+      const int c = tid + 256 * i;
+      const int key = c / CPR, ch = c % CPR;  // K: row-major order, coalesced
+      const int vkey = c % BN, vch = c / BN;  // V: key-fastest, conflict-free transpose
+      uint4 z = {0, 0, 0, 0};
+      kreg[i] = (kb + key < Lk) ? ldg16(K + kbase + (int64_t)(kb + key) * D + 8 * ch) : z;
+      vreg[i] = (kb + vkey < Lk) ? ldg16(V + kbase + (int64_t)(kb + vkey) * D + 8 * vch) : z;
+    }
+  };
+  auto sstore = [&]() {
+#pragma unroll
+    for (int i = 0; i < LPT; ++i) {
+      const int c = tid + 256 * i;
+      const int key = c / CPR, ch = c % CPR;
+      *reinterpret_cast<uint4*>(&sK[key * KP + 8 * ch]) = kreg[i];
+      const int vkey = c % BN, vch = c / BN;
+      const u16* e = reinterpret_cast<const u16*>(&vreg[i]);
+      const int pos = perm16(vkey);
+#pragma unroll
+      for (int x = 0; x < 8; ++x) sVt[(8 * vch + x) * VP + pos] = e[x];
+    }
+  };
+
+  if (kend > 0) gload(0);
+  for (int kb = 0; kb < kend; kb += BN) {
+    __syncthreads();
+    sstore();
+    __syncthreads();
+    if (kb + BN < kend) gload(kb + BN);
+    if (CAUSAL && kb > wq_hi) continue;  // every key of the tile is after every query of the wave
+
+    f32x16 s[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      s[t] = f32x16{};
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        bf16x8 a = *reinterpret_cast<const bf16x8*>(&sK[(32 * t + r32) * KP + 16 * c + 8 * g]);
+        s[t] = mfma_bf16_32x32x16(a, qf[c], s[t]);
+      }
+    }
+
+    const bool need_mask = (kb + BN > Lk) || (CAUSAL && kb + BN - 1 > wq_lo);
+    float mx = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float x = s[t][r] * sl2;
+        if (need_mask) {
+          const int key = kb + 32 * t + acc_row(r, g);
+          if (key >= Lk || (CAUSAL && key > qrow)) x = -INFINITY;
+        }
+        s[t][r] = x;
+        mx = fmaxf(mx, x);
+      }
+    mx = fmaxf(mx, wave_xor32(mx));
+    const float mnew = fmaxf(m, mx);
+    const float mb = (mnew == -INFINITY) ? 0.f : mnew;
+    const float alpha = fast_exp2(m - mb);
+    m = mnew;
+    float ps = 0.f;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = fast_exp2(s[t][r] - mb);
+        s[t][r] = p;
+        ps += p;
+      }
+    lsum = lsum * alpha + ps;
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt) acc[dt] *= alpha;
+
+    bf16x8 pb[4];
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) pb[kc][e] = (__bf16)s[kc >> 1][8 * (kc & 1) + e];
+
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+      for (int kc = 0; kc < 4; ++kc) {
+        bf16x8 a = *reinterpret_cast<const bf16x8*>(&sVt[(32 * dt + r32) * VP + 16 * kc + 8 * g]);
+        acc[dt] = mfma_bf16_32x32x16(a, pb[kc], acc[dt]);
+      }
+  }
+
+  lsum += wave_xor32(lsum);
+  if (qrow < Lq) {
+    const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+    u16* orow = O + qbase + (int64_t)qrow * D;
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; r += 4) {
+        const int d0 = 32 * dt + acc_row(r, g);
+        uint2 v;
+        v.x = pack_bf16x2(acc[dt][r] * inv, acc[dt][r + 1] * inv);
+        v.y = pack_bf16x2(acc[dt][r + 2] * inv, acc[dt][r + 3] * inv);
+        *reinterpret_cast<uint2*>(orow + d0) = v;
+      }
+    if (g == 0 && LSE) LSE[(int64_t)bh * Lq + qrow] = (m + __log2f(lsum)) * kLn2;
+  }
+}
+
+template <int D, bool CAUSAL>
+__global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void attn_fwd_f32_kernel(
+    const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
+    float* __restrict__ O, float* __restrict__ LSE, int Lq, int Lk, int BH, int nqt, int group,
+    float sl2) {
+  constexpr int BM = FWD_BM, BN = FWD_BN;
+  constexpr int P = D + 1;    // row pitch (floats): lanes on consecutive rows hit distinct banks
+  constexpr int NC = D / 2;   // k-steps of the d contraction (2 per MFMA)
+  constexpr int ND = D / 32;
+  constexpr int CPR = D / 4;  // 16-byte chunks per row
+  constexpr int LPT = BN * CPR / 256;
+  __shared__ float sK[BN * P];
+  __shared__ float sV[BN * P];
+
+  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, g = l >> 5, r32 = l & 31;
+  int qt, bh;
+  map_tile(blockIdx.x, nqt, BH, group, qt, bh, CAUSAL);
+  const int q0 = qt * BM;
+  const int qrow = q0 + 32 * w + r32;
+  const int64_t qbase = (int64_t)bh * Lq * D;
+  const int64_t kbase = (int64_t)bh * Lk * D;
+
+  float qf[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) qf[c] = (qrow < Lq) ? Q[qbase + (int64_t)qrow * D + 2 * c + g] : 0.f;
+
+  f32x16 acc[ND];
+#pragma unroll
+  for (int dt = 0; dt < ND; ++dt) acc[dt] = f32x16{};
+  float m = -INFINITY, lsum = 0.f;
+  const int kend = CAUSAL ? min(Lk, q0 + BM) : Lk;
+  const int wq_lo = q0 + 32 * w, wq_hi = wq_lo + 31;
+
+  float4 kreg[LPT], vreg[LPT];
+  auto gload = [&](int kb) {
+#pragma unroll
+    for (int i = 0; i < LPT; ++i) {
+      const int c = tid + 256 * i;
+      const int key = c / CPR, ch = c % CPR;
+      float4 z = {0.f, 0.f, 0.f, 0.f};
+      const bool in = kb + key < Lk;
+      kreg[i] = in ? *reinterpret_cast<const float4*>(K + kbase + (int64_t)(kb + key) * D + 4 * ch) : z;
+      vreg[i] = in ? *reinterpret_cast<const float4*>(V + kbase + (int64_t)(kb + key) * D + 4 * ch) : z;
+    }
+  };
+  auto sstore = [&]() {
+#pragma unroll
+    for (int i = 0; i < LPT; ++i) {
+      const int c = tid + 256 * i;
+      const int key = c / CPR, ch = c % CPR;
+      float* pk = &sK[key * P + 4 * ch];
+      float* pv = &sV[key * P + 4 * ch];
+      pk[0] = kreg[i].x; pk[1] = kreg[i].y; pk[2] = kreg[i].z; pk[3] = kreg[i].w;
+      pv[0] = vreg[i].x; pv[1] = vreg[i].y; pv[2] = vreg[i].z; pv[3] = vreg[i].w;
+    }
+  };
+
+  if (kend > 0) gload(0);
+  for (int kb = 0; kb < kend; kb += BN) {
+    __syncthreads();
+    sstore();
+    __syncthreads();
+    if (kb + BN < kend) gload(kb + BN);
+    if (CAUSAL && kb > wq_hi) continue;
+
+    f32x16 s[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      s[t] = f32x16{};
+#pragma unroll
+      for (int c = 0; c < NC; ++c) s[t] = mfma_f32_32x32x2(sK[(32 * t + r32) * P + 2 * c + g], qf[c], s[t]);
+    }
+    const bool need_mask = (kb + BN > Lk) || (CAUSAL && kb + BN - 1 > wq_lo);
+    float mx = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float x = s[t][r] * sl2;
+        if (need_mask) {
+          const int key = kb + 32 * t + acc_row(r, g);
+          if (key >= Lk || (CAUSAL && key > qrow)) x = -INFINITY;
+        }
+        s[t][r] = x;
+        mx = fmaxf(mx, x);
+      }
+    mx = fmaxf(mx, wave_xor32(mx));
+    const float mnew = fmaxf(m, mx);
+    const float mb = (mnew == -INFINITY) ? 0.f : mnew;
+    const float alpha = fast_exp2(m - mb);
+    m = mnew;
+    float ps = 0.f;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = fast_exp2(s[t][r] - mb);
+        s[t][r] = p;
+        ps += p;
+      }
+    lsum = lsum * alpha + ps;
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt) acc[dt] *= alpha;
+    // O^T += V^T P^T, two keys (one per lane half) per MFMA.
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          acc[dt] = mfma_f32_32x32x2(sV[(32 * t + acc_row(r, g)) * P + 32 * dt + r32], s[t][r], acc[dt]);
+  }
+
+  lsum += wave_xor32(lsum);
+  if (qrow < Lq) {
+    const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+    float* orow = O + qbase + (int64_t)qrow * D;
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; r += 4) {
+        float4 v = {acc[dt][r] * inv, acc[dt][r + 1] * inv, acc[dt][r + 2] * inv, acc[dt][r + 3] * inv};
+        *reinterpret_cast<float4*>(orow + 32 * dt + acc_row(r, g)) = v;
+      }
+    if (g == 0 && LSE) LSE[(int64_t)bh * Lq + qrow] = (m + __log2f(lsum)) * kLn2;
+  }
+}
+
+template <typename T, typename KernelPtr>
+static int launch_fwd(KernelPtr kern, const T* q, const T* k, const T* v, T* o, float* lse,
+                      int64_t BH, int64_t Lq, int64_t Lk, float scale, hipStream_t s) {
+  const int64_t nqt = (Lq + FWD_BM - 1) / FWD_BM;
+  const int64_t nblk = nqt * BH;
+  if (nblk > 0x7fffffff) return fail(TT_ERR_ARG, "attention forward: grid too large");
+  const int group = pick_group(BH, nqt, 64);
+  hipLaunchKernelGGL(kern, dim3((unsigned)nblk), dim3(256), 0, s, q, k, v, o, lse, (int)Lq, (int)Lk,
+                     (int)BH, (int)nqt, group, scale * kLog2e);
+  TT_LAUNCH_CHECK("attention forward launch");
+  return ok();
+}
+
+}  // namespace tt
+
+using namespace tt;
+
+#define TT_FWD_DISPATCH(KERNEL, T)                                                              \
+  switch (d * 2 + (causal ? 1 : 0)) {                                                           \
+    case 64: return launch_fwd(KERNEL<32, false>, q, k, v, o, lse, BH, Lq, Lk, scale, st);      \
+    case 65: return launch_fwd(KERNEL<32, true>, q, k, v, o, lse, BH, Lq, Lk, scale, st);       \
+    case 128: return launch_fwd(KERNEL<64, false>, q, k, v, o, lse, BH, Lq, Lk, scale, st);     \
+    case 129: return launch_fwd(KERNEL<64, true>, q, k, v, o, lse, BH, Lq, Lk, scale, st);      \
+    case 256: return launch_fwd(KERNEL<128, false>, q, k, v, o, lse, BH, Lq, Lk, scale, st);    \
+    case 257: return launch_fwd(KERNEL<128, true>, q, k, v, o, lse, BH, Lq, Lk, scale, st);     \
+    default: return fail(TT_ERR_UNSUPPORTED, "attention forward: unsupported head dim");       \
+  }
+
+extern "C" int tt_attn_fwd_f32(const float* q, const float* k, const float* v, float* o, float* lse,
+                               int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t d, float scale,
+                               int causal, void* stream) {
+  int rc = check_attn_shape("tt_attn_fwd_f32", B, H, Lq, Lk, d, causal);
+  if (rc) return rc;
+  const int64_t BH = B * H;
+  if (BH == 0 || Lq == 0) return ok();
+  if (!q || !k || !v || !o) return fail(TT_ERR_ARG, "tt_attn_fwd_f32: null pointer");
+  if ((rc = ensure_init())) return rc;
+  hipStream_t st = stream_or_default(stream);
+  TT_FWD_DISPATCH(attn_fwd_f32_kernel, float)
+}
+
+extern "C" int tt_attn_fwd_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o,
+                                float* lse, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t d,
+                                float scale, int causal, void* stream) {
+  int rc = check_attn_shape("tt_attn_fwd_bf16", B, H, Lq, Lk, d, causal);
+  if (rc) return rc;
+  const int64_t BH = B * H;
+  if (BH == 0 || Lq == 0) return ok();
+  if (!q || !k || !v || !o) return fail(TT_ERR_ARG, "tt_attn_fwd_bf16: null pointer");
+  if ((rc = ensure_init())) return rc;
+  hipStream_t st = stream_or_default(stream);
+  TT_FWD_DISPATCH(attn_fwd_bf16_kernel, u16)
+}

@@ -1,0 +1,63 @@
+// Workgroup -> (tile, head) mapping and host-side argument checks shared by
+// the attention launchers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+
+#include "tt_internal.h"
+
+namespace tt {
+
+// MI355X dispatches consecutive workgroup ids round-robin over its 8 XCDs,
+// each with a private L2.  When the head count is a multiple of 8 the tiles
+// of head bh all run on XCD bh % 8 and each XCD works through `group` heads
+// at a time, so the K/V (or Q/dO) of the heads in flight stay in that L2.
+// Inside a group the tile rank runs from the most expensive causal tile
+// (the last one) to the cheapest, which evens out the tail.
+__device__ __forceinline__ void map_tile(int id, int ntile, int BH, int group, int& tile, int& bh,
+                                         bool heavy_last) {
+  int rank;
+  if ((BH & 7) == 0 && group > 0) {
+    int xcd = id & 7, t = id >> 3;
+    int per = group * ntile;
+    int gi = t / per, r = t - gi * per;
+    rank = r / group;
+    int hg = r - rank * group;
+    bh = xcd + 8 * (gi * group + hg);
+  } else {
+    rank = id / BH;
+    bh = id - rank * BH;
+  }
+  tile = heavy_last ? (ntile - 1 - rank) : rank;
+}
+
+// Largest divisor of BH/8 that keeps about `target` workgroups of one XCD on
+// `group` heads at once (0 disables the XCD mapping).
+inline int pick_group(int64_t BH, int64_t ntile, int64_t target) {
+  if (BH % 8 != 0) return 0;
+  int64_t per_xcd = BH / 8;
+  int64_t want = target / (ntile > 0 ? ntile : 1);
+  if (want < 1) want = 1;
+  int64_t best = 1;
+  for (int64_t gsz = 1; gsz <= per_xcd; ++gsz)
+    if (per_xcd % gsz == 0 && gsz <= want) best = gsz;
+  return (int)best;
+}
+
+inline int check_attn_shape(const char* fn, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t d,
+                            int causal) {
+  std::string f(fn);
+  if (B < 0 || H < 0 || Lq < 0 || Lk < 0) return fail(TT_ERR_ARG, f + ": negative dimension");
+  if (d != 32 && d != 64 && d != 128)
+    return fail(TT_ERR_UNSUPPORTED, f + ": head dim must be 32, 64 or 128 (got " + std::to_string(d) + ")");
+  if (causal && Lq != Lk) return fail(TT_ERR_ARG, f + ": causal mask needs Lq == Lk");
+  if (Lq > 0 && Lk == 0 && B * H > 0) return fail(TT_ERR_ARG, f + ": softmax over zero keys");
+  if (Lq > (int64_t(1) << 30) || Lk > (int64_t(1) << 30)) return fail(TT_ERR_ARG, f + ": sequence too long");
+  if (B * H > (int64_t(1) << 24)) return fail(TT_ERR_ARG, f + ": too many heads");
+  return TT_OK;
+}
+
+}  // namespace tt

@@ -1,0 +1,30 @@
+// Module `myLayer`: the attention entry points, bound in the style of
+// Task3/Tinytensor/src/bind_Layer.cpp:10-24 (free functions over TinyTensor
+// references), with float and bf16 overloads.
+#include <pybind11/pybind11.h>
+#include <pybind11/stl.h>
+
+#include "layers.h"
+
+namespace py = pybind11;
+
+PYBIND11_MODULE(myLayer, m) {
+  m.doc() = "myLayer: fused attention for MI355X (gfx950)";
+  // The tensor classes are registered by myTensor; import it so that callers
+  // can use myLayer first.
+  py::module_::import("myTensor");
+  m.def("AttentionForward", &AttentionForward<float>, py::arg("q"), py::arg("k"), py::arg("v"), py::arg("out"),
+        py::arg("lse"), py::arg("scale"), py::arg("causal"));
+  m.def("AttentionForward", &AttentionForward<bf16>, py::arg("q"), py::arg("k"), py::arg("v"), py::arg("out"),
+        py::arg("lse"), py::arg("scale"), py::arg("causal"));
+  m.def("AttentionBackward", &AttentionBackward<float>, py::arg("q"), py::arg("k"), py::arg("v"), py::arg("out"),
+        py::arg("lse"), py::arg("grad_out"), py::arg("grad_q"), py::arg("grad_k"), py::arg("grad_v"),
+        py::arg("scale"), py::arg("causal"));
+  m.def("AttentionBackward", &AttentionBackward<bf16>, py::arg("q"), py::arg("k"), py::arg("v"), py::arg("out"),
+        py::arg("lse"), py::arg("grad_out"), py::arg("grad_q"), py::arg("grad_k"), py::arg("grad_v"),
+        py::arg("scale"), py::arg("causal"));
+  m.def("AttentionDecode", &AttentionDecode<float>, py::arg("q"), py::arg("k_cache"), py::arg("v_cache"),
+        py::arg("out"), py::arg("scale"));
+  m.def("AttentionDecode", &AttentionDecode<bf16>, py::arg("q"), py::arg("k_cache"), py::arg("v_cache"),
+        py::arg("out"), py::arg("scale"));
+}

@@ -1,0 +1,28 @@
+// Attention layer functions of the `myLayer` module.
+//
+// They follow the reference's layer convention (FcForward/FcBackward,
+// Task3/Tinytensor/src/Layers.h:8-26, Layers.cu:9-79): inputs are const
+// TinyTensor references on the "gpu" device, outputs are non-const
+// references that the callee resizes in place (Layers.cu:25, 52-57), float
+// instantiations plus bf16 ones for the attention path.
+#pragma once
+
+#include "tinytensor.h"
+
+// O = softmax(scale * Q K^T + M) V and LSE (natural log, fp32 [B,H,Lq]).
+// q [B,H,Lq,d], k/v [B,H,Lk,d]; causal -> M = -inf where key > query.
+template <typename T>
+void AttentionForward(const TinyTensor<T>& q, const TinyTensor<T>& k, const TinyTensor<T>& v,
+                      TinyTensor<T>& out, TinyTensor<float>& lse, float scale, bool causal);
+
+// dQ, dK, dV for upstream gradient grad_out from the saved out and lse.
+template <typename T>
+void AttentionBackward(const TinyTensor<T>& q, const TinyTensor<T>& k, const TinyTensor<T>& v,
+                       const TinyTensor<T>& out, const TinyTensor<float>& lse,
+                       const TinyTensor<T>& grad_out, TinyTensor<T>& grad_q, TinyTensor<T>& grad_k,
+                       TinyTensor<T>& grad_v, float scale, bool causal);
+
+// Single-query decode: q [B,H,1,d], caches [B,H,Lkv,d] -> out [B,H,1,d].
+template <typename T>
+void AttentionDecode(const TinyTensor<T>& q, const TinyTensor<T>& k_cache, const TinyTensor<T>& v_cache,
+                     TinyTensor<T>& out, float scale);

@@ -1,0 +1,454 @@
+// TinyTensor device runtime for MI355X: errors, stream, caching allocator,
+// copies, events and the elementwise kernels behind TinyTensor's methods.
+//
+// The reference allocates with cudaMalloc/cudaFree on every construction and
+// synchronises after every launch (src/Tinytensor.cu:21,90,146).  Here all
+// work is ordered on one library stream; host-visible copies wait for it.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+
+#include "tt_internal.h"
+
+namespace tt {
+
+static thread_local std::string g_err;
+
+int fail(int code, const std::string& msg) {
+  g_err = msg;
+  return code;
+}
+int ok() {
+  g_err.clear();
+  return TT_OK;
+}
+int hip_fail(hipError_t e, const char* what) {
+  std::string m = std::string("HIP error in ") + what + ": " + hipGetErrorName(e) + " (" +
+                  hipGetErrorString(e) + ")";
+  int code = (e == hipErrorOutOfMemory) ? TT_ERR_NOMEM : TT_ERR_HIP;
+  return fail(code, m);
+}
+
+static std::mutex g_mu;
+static bool g_inited = false;
+static int g_device = 0;
+static hipStream_t g_stream = nullptr;
+
+int ensure_init() {
+  if (g_inited) return TT_OK;
+  return tt_init(g_device);
+}
+
+hipStream_t stream_or_default(void* s) {
+  return s ? static_cast<hipStream_t>(s) : g_stream;
+}
+
+// ---------------------------------------------------------------- allocator
+// Size classes: 512 B granules below 1 MiB, 2 MiB granules above.  Freed
+// blocks go to a multimap keyed by class size and are reused first-fit
+// (smallest class >= request, at most 2x the request to bound waste).
+struct Alloc {
+  std::multimap<size_t, void*> free_blocks;
+  std::unordered_map<void*, size_t> live;  // ptr -> class size
+  size_t in_use = 0, cached = 0;
+};
+static Alloc g_alloc;
+
+static size_t size_class(size_t bytes) {
+  if (bytes == 0) bytes = 1;
+  const size_t small = 512, big = size_t(2) << 20;
+  if (bytes < (size_t(1) << 20)) return (bytes + small - 1) / small * small;
+  return (bytes + big - 1) / big * big;
+}
+
+static int alloc_block(size_t bytes, void** ptr) {
+  size_t cls = size_class(bytes);
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    auto it = g_alloc.free_blocks.lower_bound(cls);
+    if (it != g_alloc.free_blocks.end() && it->first <= 2 * cls) {
+      *ptr = it->second;
+      size_t c = it->first;
+      g_alloc.free_blocks.erase(it);
+      g_alloc.live[*ptr] = c;
+      g_alloc.cached -= c;
+      g_alloc.in_use += c;
+      return TT_OK;
+    }
+  }
+  void* p = nullptr;
+  hipError_t e = hipMalloc(&p, cls);
+  if (e != hipSuccess) {
+    // Return cached blocks to HIP and retry once.
+    (void)hipGetLastError();
+    tt_empty_cache();
+    e = hipMalloc(&p, cls);
+    if (e != hipSuccess) {
+      (void)hipGetLastError();
+      return fail(TT_ERR_NOMEM, "tt_malloc: hipMalloc of " + std::to_string(cls) +
+                                    " bytes failed: " + hipGetErrorString(e));
+    }
+  }
+  std::lock_guard<std::mutex> lk(g_mu);
+  g_alloc.live[p] = cls;
+  g_alloc.in_use += cls;
+  *ptr = p;
+  return TT_OK;
+}
+
+// ---------------------------------------------------------------- workspace
+static void* g_ws[4] = {nullptr, nullptr, nullptr, nullptr};
+static size_t g_ws_bytes[4] = {0, 0, 0, 0};
+
+int workspace(int slot, size_t bytes, void** ptr) {
+  if (slot < 0 || slot >= 4) return fail(TT_ERR_ARG, "workspace: bad slot");
+  if (bytes <= g_ws_bytes[slot] && g_ws[slot]) {
+    *ptr = g_ws[slot];
+    return TT_OK;
+  }
+  if (g_ws[slot]) {
+    // The old buffer may still be read by queued work on the stream.
+    TT_HIP(hipStreamSynchronize(g_stream));
+    tt_free(g_ws[slot]);
+    g_ws[slot] = nullptr;
+    g_ws_bytes[slot] = 0;
+  }
+  int rc = alloc_block(bytes, &g_ws[slot]);
+  if (rc) return rc;
+  g_ws_bytes[slot] = bytes;
+  *ptr = g_ws[slot];
+  return TT_OK;
+}
+
+// ---------------------------------------------------------------- elementwise
+__device__ __forceinline__ uint64_t splitmix64(uint64_t x) {
+  x += 0x9E3779B97F4A7C15ull;
+  x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+  x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+  return x ^ (x >> 31);
+}
+
+// Uniform in [0, 1) with 24 bits from a 64-bit hash.
+__device__ __forceinline__ float u01(uint64_t h) { return (float)(h >> 40) * (1.0f / 16777216.0f); }
+
+__device__ __forceinline__ float bf2f(uint16_t b) { return __uint_as_float(uint32_t(b) << 16); }
+__device__ __forceinline__ uint16_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return uint16_t((u >> 16) | 0x40);  // quiet NaN
+  u += 0x7fffu + ((u >> 16) & 1u);                                          // RNE
+  return uint16_t(u >> 16);
+}
+
+template <typename T> struct Num {
+  __device__ static float ld(const T* p, int64_t i) { return (float)p[i]; }
+  __device__ static void st(T* p, int64_t i, double v) { p[i] = (T)v; }
+};
+template <> struct Num<uint16_t> {  // bf16 storage
+  __device__ static float ld(const uint16_t* p, int64_t i) { return bf2f(p[i]); }
+  __device__ static void st(uint16_t* p, int64_t i, double v) { p[i] = f2bf((float)v); }
+};
+template <> struct Num<double> {
+  __device__ static double ld(const double* p, int64_t i) { return p[i]; }
+  __device__ static void st(double* p, int64_t i, double v) { p[i] = v; }
+};
+
+template <typename T>
+__global__ void k_elementwise(int op, T* c, const T* a, const T* b, int64_t n, double alpha,
+                              double beta, uint64_t seed) {
+  int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    double r = 0.0;
+    switch (op) {
+      case TT_EW_ADD: r = (double)Num<T>::ld(a, i) + (double)Num<T>::ld(b, i); break;
+      case TT_EW_SUB: r = (double)Num<T>::ld(a, i) - (double)Num<T>::ld(b, i); break;
+      case TT_EW_FILL: r = alpha; break;
+      case TT_EW_NEG: r = -(double)Num<T>::ld(a, i); break;
+      case TT_EW_SCALE: r = (double)Num<T>::ld(a, i) * alpha; break;
+      case TT_EW_RELU: { double x = Num<T>::ld(a, i); r = x > 0 ? x : 0; } break;
+      case TT_EW_RELU_BWD: r = Num<T>::ld(a, i) > 0 ? (double)Num<T>::ld(b, i) : 0.0; break;
+      case TT_EW_SIGMOID: r = 1.0 / (1.0 + exp(-(double)Num<T>::ld(a, i))); break;
+      case TT_EW_SIGMOID_BWD: {
+        double s = 1.0 / (1.0 + exp(-(double)Num<T>::ld(a, i)));
+        r = s * (1.0 - s) * (double)Num<T>::ld(b, i);
+      } break;
+      case TT_EW_UNIFORM: {
+        double u = u01(splitmix64(seed ^ splitmix64((uint64_t)i)));
+        r = alpha + (beta - alpha) * u;
+      } break;
+    }
+    Num<T>::st(c, i, r);
+  }
+}
+// Integer storage: do integer arithmetic where it matters (add/sub/neg/scale).
+template <>
+__global__ void k_elementwise<int32_t>(int op, int32_t* c, const int32_t* a, const int32_t* b,
+                                       int64_t n, double alpha, double beta, uint64_t seed) {
+  int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    int32_t r = 0;
+    switch (op) {
+      case TT_EW_ADD: r = a[i] + b[i]; break;
+      case TT_EW_SUB: r = a[i] - b[i]; break;
+      case TT_EW_FILL: r = (int32_t)alpha; break;
+      case TT_EW_NEG: r = -a[i]; break;
+      case TT_EW_SCALE: r = (int32_t)(a[i] * (int32_t)alpha); break;
+      case TT_EW_RELU: r = a[i] > 0 ? a[i] : 0; break;
+      case TT_EW_RELU_BWD: r = a[i] > 0 ? b[i] : 0; break;
+      case TT_EW_SIGMOID: r = (int32_t)(1.0 / (1.0 + exp(-(double)a[i]))); break;
+      case TT_EW_SIGMOID_BWD: {
+        double s = 1.0 / (1.0 + exp(-(double)a[i]));
+        r = (int32_t)(s * (1.0 - s) * b[i]);
+      } break;
+      case TT_EW_UNIFORM: {
+        // Inclusive integer range [alpha, beta] like std::uniform_int_distribution.
+        int64_t lo = (int64_t)alpha, hi = (int64_t)beta;
+        uint64_t span = (uint64_t)(hi - lo + 1);
+        r = (int32_t)(lo + (int64_t)(splitmix64(seed ^ splitmix64((uint64_t)i)) % span));
+      } break;
+    }
+    c[i] = r;
+  }
+}
+
+// scale * N(0,1) by Box-Muller on two 24-bit uniforms of splitmix64(seed, i).
+template <typename T>
+__global__ void k_fill_normal(T* dst, int64_t n, uint64_t seed, float scale) {
+  int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    uint64_t h = splitmix64(seed * 0x100000001B3ull ^ splitmix64((uint64_t)i));
+    float u1 = ((float)(h >> 40) + 0.5f) * (1.0f / 16777216.0f);
+    float u2 = (float)((h >> 16) & 0xFFFFFFu) * (1.0f / 16777216.0f);
+    float z = sqrtf(-2.0f * logf(u1)) * cosf(6.283185307179586f * u2);
+    Num<T>::st(dst, i, (double)(z * scale));
+  }
+}
+
+static int grid_for(int64_t n) {
+  int64_t g = (n + 255) / 256;
+  if (g > 65536) g = 65536;
+  if (g < 1) g = 1;
+  return (int)g;
+}
+
+}  // namespace tt
+
+using namespace tt;
+
+extern "C" {
+
+const char* tt_last_error(void) { return g_err.c_str(); }
+const char* tt_version(void) { return "tinytensor-mi355x 0.1 (gfx950)"; }
+
+int tt_device_count(int* n) {
+  if (!n) return fail(TT_ERR_ARG, "tt_device_count: null pointer");
+  int c = 0;
+  if (hipGetDeviceCount(&c) != hipSuccess) {
+    (void)hipGetLastError();
+    c = 0;
+  }
+  *n = c;
+  return ok();
+}
+
+int tt_init(int device) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (g_inited) {
+    if (device != g_device) return fail(TT_ERR_ARG, "tt_init: library already bound to another device");
+    return TT_OK;
+  }
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n == 0) {
+    (void)hipGetLastError();
+    return fail(TT_ERR_HIP, "tt_init: no HIP device available");
+  }
+  if (device < 0 || device >= n) return fail(TT_ERR_ARG, "tt_init: device index out of range");
+  TT_HIP(hipSetDevice(device));
+  // Default priority on purpose: one stream, ordinary priority.
+  TT_HIP(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
+  g_device = device;
+  g_inited = true;
+  return ok();
+}
+
+void* tt_stream(void) {
+  if (ensure_init() != TT_OK) return nullptr;
+  return (void*)g_stream;
+}
+
+int tt_malloc(void** ptr, size_t bytes) {
+  if (!ptr) return fail(TT_ERR_ARG, "tt_malloc: null pointer");
+  *ptr = nullptr;
+  int rc = ensure_init();
+  if (rc) return rc;
+  rc = alloc_block(bytes, ptr);
+  if (rc) return rc;
+  return ok();
+}
+
+int tt_free(void* ptr) {
+  if (!ptr) return TT_OK;
+  std::lock_guard<std::mutex> lk(g_mu);
+  auto it = g_alloc.live.find(ptr);
+  if (it == g_alloc.live.end()) return fail(TT_ERR_ARG, "tt_free: pointer not from tt_malloc");
+  size_t c = it->second;
+  g_alloc.live.erase(it);
+  g_alloc.in_use -= c;
+  // Work queued on the library stream that still reads this block runs
+  // before any later user of the block on the same stream.
+  g_alloc.free_blocks.emplace(c, ptr);
+  g_alloc.cached += c;
+  return TT_OK;
+}
+
+int tt_empty_cache(void) {
+  std::multimap<size_t, void*> blocks;
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    blocks.swap(g_alloc.free_blocks);
+    g_alloc.cached = 0;
+  }
+  if (!g_inited) return TT_OK;
+  if (!blocks.empty()) TT_HIP(hipStreamSynchronize(g_stream));
+  for (auto& kv : blocks) TT_HIP(hipFree(kv.second));
+  return TT_OK;
+}
+
+int tt_mem_stats(size_t* in_use, size_t* cached) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (in_use) *in_use = g_alloc.in_use;
+  if (cached) *cached = g_alloc.cached;
+  return TT_OK;
+}
+
+int tt_memcpy_h2d(void* dst, const void* src, size_t bytes) {
+  if (bytes == 0) return TT_OK;
+  if (!dst || !src) return fail(TT_ERR_ARG, "tt_memcpy_h2d: null pointer");
+  int rc = ensure_init();
+  if (rc) return rc;
+  TT_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, g_stream));
+  TT_HIP(hipStreamSynchronize(g_stream));
+  return ok();
+}
+
+int tt_memcpy_d2h(void* dst, const void* src, size_t bytes) {
+  if (bytes == 0) return TT_OK;
+  if (!dst || !src) return fail(TT_ERR_ARG, "tt_memcpy_d2h: null pointer");
+  int rc = ensure_init();
+  if (rc) return rc;
+  TT_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, g_stream));
+  TT_HIP(hipStreamSynchronize(g_stream));
+  return ok();
+}
+
+int tt_memcpy_d2d(void* dst, const void* src, size_t bytes) {
+  if (bytes == 0) return TT_OK;
+  if (!dst || !src) return fail(TT_ERR_ARG, "tt_memcpy_d2d: null pointer");
+  int rc = ensure_init();
+  if (rc) return rc;
+  TT_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, g_stream));
+  return ok();
+}
+
+int tt_memset(void* ptr, int value, size_t bytes) {
+  if (bytes == 0) return TT_OK;
+  if (!ptr) return fail(TT_ERR_ARG, "tt_memset: null pointer");
+  int rc = ensure_init();
+  if (rc) return rc;
+  TT_HIP(hipMemsetAsync(ptr, value, bytes, g_stream));
+  return ok();
+}
+
+int tt_sync(void) {
+  int rc = ensure_init();
+  if (rc) return rc;
+  TT_HIP(hipStreamSynchronize(g_stream));
+  return ok();
+}
+
+int tt_event_create(void** ev) {
+  if (!ev) return fail(TT_ERR_ARG, "tt_event_create: null pointer");
+  int rc = ensure_init();
+  if (rc) return rc;
+  hipEvent_t e;
+  TT_HIP(hipEventCreate(&e));
+  *ev = (void*)e;
+  return ok();
+}
+int tt_event_record(void* ev, void* stream) {
+  if (!ev) return fail(TT_ERR_ARG, "tt_event_record: null event");
+  TT_HIP(hipEventRecord((hipEvent_t)ev, stream_or_default(stream)));
+  return ok();
+}
+int tt_event_elapsed_ms(float* ms, void* start, void* stop) {
+  if (!ms || !start || !stop) return fail(TT_ERR_ARG, "tt_event_elapsed_ms: null pointer");
+  TT_HIP(hipEventSynchronize((hipEvent_t)stop));
+  TT_HIP(hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)stop));
+  return ok();
+}
+int tt_event_destroy(void* ev) {
+  if (!ev) return TT_OK;
+  TT_HIP(hipEventDestroy((hipEvent_t)ev));
+  return ok();
+}
+
+int tt_elementwise(int op, int dtype, void* c, const void* a, const void* b, int64_t n,
+                   double alpha, double beta, uint64_t seed, void* stream) {
+  if (n < 0) return fail(TT_ERR_ARG, "tt_elementwise: negative size");
+  if (n == 0) return TT_OK;
+  if (op < TT_EW_ADD || op > TT_EW_UNIFORM) return fail(TT_ERR_ARG, "tt_elementwise: bad op");
+  bool need_a = !(op == TT_EW_FILL || op == TT_EW_UNIFORM);
+  bool need_b = (op == TT_EW_ADD || op == TT_EW_SUB || op == TT_EW_RELU_BWD || op == TT_EW_SIGMOID_BWD);
+  if (!c || (need_a && !a) || (need_b && !b)) return fail(TT_ERR_ARG, "tt_elementwise: null pointer");
+  int rc = ensure_init();
+  if (rc) return rc;
+  hipStream_t s = stream_or_default(stream);
+  int g = grid_for(n);
+  switch (dtype) {
+    case TT_F32:
+      hipLaunchKernelGGL(k_elementwise<float>, dim3(g), dim3(256), 0, s, op, (float*)c,
+                         (const float*)a, (const float*)b, n, alpha, beta, seed);
+      break;
+    case TT_F64:
+      hipLaunchKernelGGL(k_elementwise<double>, dim3(g), dim3(256), 0, s, op, (double*)c,
+                         (const double*)a, (const double*)b, n, alpha, beta, seed);
+      break;
+    case TT_I32:
+      hipLaunchKernelGGL(k_elementwise<int32_t>, dim3(g), dim3(256), 0, s, op, (int32_t*)c,
+                         (const int32_t*)a, (const int32_t*)b, n, alpha, beta, seed);
+      break;
+    case TT_BF16:
+      hipLaunchKernelGGL(k_elementwise<uint16_t>, dim3(g), dim3(256), 0, s, op, (uint16_t*)c,
+                         (const uint16_t*)a, (const uint16_t*)b, n, alpha, beta, seed);
+      break;
+    default:
+      return fail(TT_ERR_ARG, "tt_elementwise: bad dtype");
+  }
+  TT_LAUNCH_CHECK("tt_elementwise");
+  return ok();
+}
+
+int tt_fill_normal(int dtype, void* dst, int64_t n, uint64_t seed, float scale, void* stream) {
+  if (n < 0) return fail(TT_ERR_ARG, "tt_fill_normal: negative size");
+  if (n == 0) return TT_OK;
+  if (!dst) return fail(TT_ERR_ARG, "tt_fill_normal: null pointer");
+  int rc = ensure_init();
+  if (rc) return rc;
+  hipStream_t s = stream_or_default(stream);
+  int g = grid_for(n);
+  if (dtype == TT_F32)
+    hipLaunchKernelGGL(k_fill_normal<float>, dim3(g), dim3(256), 0, s, (float*)dst, n, seed, scale);
+  else if (dtype == TT_BF16)
+    hipLaunchKernelGGL(k_fill_normal<uint16_t>, dim3(g), dim3(256), 0, s, (uint16_t*)dst, n, seed, scale);
+  else
+    return fail(TT_ERR_ARG, "tt_fill_normal: dtype must be f32 or bf16");
+  TT_LAUNCH_CHECK("tt_fill_normal");
+  return ok();
+}
+
+}  // extern "C"

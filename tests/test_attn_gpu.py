@@ -1,0 +1,293 @@
+"""GPU parity tests: the HIP kernels, called through the C-ABI
+(include/tt_attn.h via pku-aiprogramming_amd/tt_capi.py), against the CPU
+oracle (oracle/attn_oracle.py, float64 ground truth) on seeded inputs.
+
+Error metric (per output tensor): max|x - ref| / max|ref| with ref the
+float64 oracle on the exact (bf16-rounded) inputs.  Tolerances, as stated by
+the target: fp32 <= 1e-4, bf16 with fp32 accumulation <= 2e-2.
+
+Full-size configs are checked on sampled heads against the oracle and, over
+every head, through size-independent identities of the exact result:
+  sum_j dV_j = sum_i dO_i      (rows of P sum to 1)
+  sum_j dK_j = 0               (rows of dS sum to 0)
+  causal: O[0] = V[0] and LSE[0] = s q_0 . k_0
+"""
+import math
+import sys
+
+import numpy as np
+import pytest
+
+from oracle import attn_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+TOL = orc.TOL
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def capi():
+    import tt_capi
+
+    L = tt_capi.lib()
+    assert L.device_count() >= 1, "no HIP device visible"
+    return tt_capi
+
+
+def _run_fwd(capi, x, dtype, scale, causal, want_lse=True):
+    q, k, v = x["q"], x["k"], x["v"]
+    B, H, Lq, d = q.shape
+    dq = capi.DeviceBuffer.from_numpy(q, dtype)
+    dk = capi.DeviceBuffer.from_numpy(k, dtype)
+    dv = capi.DeviceBuffer.from_numpy(v, dtype)
+    do = capi.DeviceBuffer(q.shape, dtype)
+    dl = capi.DeviceBuffer((B, H, Lq), "f32") if want_lse else None
+    capi.attn_fwd(dq, dk, dv, do, dl, scale, causal)
+    capi.lib().sync()
+    return dict(q=dq, k=dk, v=dv, o=do, lse=dl)
+
+
+def _run_bwd(capi, bufs, dout, dtype, scale, causal):
+    ddo = capi.DeviceBuffer.from_numpy(dout, dtype)
+    gq = capi.DeviceBuffer(bufs["q"].shape, dtype)
+    gk = capi.DeviceBuffer(bufs["k"].shape, dtype)
+    gv = capi.DeviceBuffer(bufs["v"].shape, dtype)
+    capi.attn_bwd(bufs["q"], bufs["k"], bufs["v"], bufs["o"], bufs["lse"], ddo, gq, gk, gv, scale, causal)
+    capi.lib().sync()
+    return gq.download(), gk.download(), gv.download()
+
+
+def _check(name, x, ref, tol):
+    err = orc.max_rel_err(x, ref)
+    _say(f"  {name}: max-rel-err {err:.3e} (tol {tol:g})")
+    assert err <= tol, f"{name}: {err:.3e} > {tol:g}"
+    return err
+
+
+# ------------------------------------------------------------------ configs
+
+def test_c1_fp32_forward(capi):
+    cfg = orc.CONFIGS[1]
+    _say("c1: fp32 fwd B=1 H=1 L=64 d=32")
+    g = np.load(orc_golden("c1_fwd.npz"))
+    x = {n: g[n] for n in ("q", "k", "v")}
+    b = _run_fwd(capi, x, "f32", cfg.scale, False)
+    _check("O", b["o"].download(), g["o"], TOL["f32"])
+    _check("LSE", b["lse"].download(), g["lse"], TOL["f32"])
+
+
+def test_c2_fp32_fwd_bwd(capi):
+    cfg = orc.CONFIGS[2]
+    _say("c2: fp32 fwd+bwd B=8 H=8 L=256 d=64")
+    x = orc.seeded_inputs(cfg)
+    b = _run_fwd(capi, x, "f32", cfg.scale, False)
+    o_ref, lse_ref = orc.attn_fwd_f64(x["q"], x["k"], x["v"], cfg.scale, False)
+    _check("O", b["o"].download(), o_ref, TOL["f32"])
+    _check("LSE", b["lse"].download(), lse_ref, TOL["f32"])
+    dq, dk, dv = _run_bwd(capi, b, x["do"], "f32", cfg.scale, False)
+    rq, rk, rv = orc.attn_bwd_f64(x["q"], x["k"], x["v"], x["do"], cfg.scale, False)
+    _check("dQ", dq, rq, TOL["f32"])
+    _check("dK", dk, rk, TOL["f32"])
+    _check("dV", dv, rv, TOL["f32"])
+    # the committed torch-written golden heads as a second anchor
+    gd = np.load(orc_golden("c2_fwdbwd.npz"))
+    for n, a in (("o", b["o"].download()), ("dq", dq), ("dk", dk), ("dv", dv)):
+        heads = np.stack([a[i, j] for i, j in gd["heads"]])
+        _check(f"golden {n}", heads, gd[n + "_heads"], TOL["f32"])
+
+
+def _identities(name, x, o, lse, dq, dk, dv, scale, causal, tol):
+    """Size-independent properties over every head (see module docstring)."""
+    do = x["do"].astype(np.float64)
+    sum_dv = dv.astype(np.float64).sum(axis=2)
+    _check(f"{name} sum_j dV_j = sum_i dO_i", sum_dv, do.sum(axis=2), tol)
+    # sum_j dK_j = 0: compare against the scale of dK itself
+    sum_dk = np.abs(dk.astype(np.float64).sum(axis=2)).max()
+    ref_scale = np.abs(dk.astype(np.float64)).sum(axis=2).max()
+    _say(f"  {name} |sum_j dK_j| / sum_j |dK_j| = {sum_dk / ref_scale:.3e}")
+    assert sum_dk <= tol * ref_scale
+    if causal:
+        _check(f"{name} O[0] = V[0]", o[:, :, 0], x["v"][:, :, 0], tol)
+        s00 = scale * np.einsum("bhd,bhd->bh", x["q"][:, :, 0].astype(np.float64), x["k"][:, :, 0].astype(np.float64))
+        _check(f"{name} LSE[0] = s q0.k0", lse[:, :, 0], s00, tol)
+
+
+def _sampled_heads(name, x, o, lse, dq, dk, dv, scale, causal, heads, tol):
+    for (bb, hh) in heads:
+        q, k, v = x["q"][bb, hh], x["k"][bb, hh], x["v"][bb, hh]
+        o_ref, l_ref = orc.attn_fwd_f64(q, k, v, scale, causal)
+        rq, rk, rv = orc.attn_bwd_f64(q, k, v, x["do"][bb, hh], scale, causal)
+        _say(f" {name} head ({bb},{hh})")
+        _check("O", o[bb, hh], o_ref, tol)
+        _check("LSE", lse[bb, hh], l_ref, tol)
+        _check("dQ", dq[bb, hh], rq, tol)
+        _check("dK", dk[bb, hh], rk, tol)
+        _check("dV", dv[bb, hh], rv, tol)
+
+
+def test_c3_bf16_causal_fwd_bwd(capi):
+    cfg = orc.CONFIGS[3]
+    _say("c3: bf16 causal fwd+bwd B=16 H=16 L=1024 d=64")
+    x = orc.seeded_inputs(cfg)
+    b = _run_fwd(capi, x, "bf16", cfg.scale, True)
+    o, lse = b["o"].download(), b["lse"].download()
+    dq, dk, dv = _run_bwd(capi, b, x["do"], "bf16", cfg.scale, True)
+    _sampled_heads("c3", x, o, lse, dq, dk, dv, cfg.scale, True, [(0, 0), (7, 3), (15, 15)], TOL["bf16"])
+    _identities("c3", x, o, lse, dq, dk, dv, cfg.scale, True, TOL["bf16"])
+
+
+def test_c5_bf16_causal_fwd_bwd(capi):
+    cfg = orc.CONFIGS[5]
+    _say("c5: bf16 causal fwd+bwd B=4 H=32 L=4096 d=128")
+    x = orc.seeded_inputs(cfg)
+    b = _run_fwd(capi, x, "bf16", cfg.scale, True)
+    o, lse = b["o"].download(), b["lse"].download()
+    dq, dk, dv = _run_bwd(capi, b, x["do"], "bf16", cfg.scale, True)
+    _sampled_heads("c5", x, o, lse, dq, dk, dv, cfg.scale, True, [(0, 0), (3, 31)], TOL["bf16"])
+    _identities("c5", x, o, lse, dq, dk, dv, cfg.scale, True, TOL["bf16"])
+
+
+def test_c4_bf16_decode(capi):
+    """Full-size decode.  K/V (2^31 elements each) are filled on the device by
+    the library's counter-based N(0,1) generator; sampled heads are downloaded
+    and checked against the oracle, and every head against the forward kernel
+    run with Lq = 1 (same inputs)."""
+    cfg = orc.CONFIGS[4]
+    B, H, Lkv, d = cfg.B, cfg.H, cfg.Lk, cfg.d
+    _say("c4: bf16 decode B=64 H=32 Lkv=8192 d=128")
+    q = capi.DeviceBuffer((B, H, 1, d), "bf16")
+    k = capi.DeviceBuffer((B, H, Lkv, d), "bf16")
+    v = capi.DeviceBuffer((B, H, Lkv, d), "bf16")
+    q.fill_normal(40)
+    k.fill_normal(41)
+    v.fill_normal(42)
+    o = capi.DeviceBuffer((B, H, 1, d), "bf16")
+    lse = capi.DeviceBuffer((B, H), "f32")
+    capi.attn_decode(q, k, v, o, lse, cfg.scale)
+    o2 = capi.DeviceBuffer((B, H, 1, d), "bf16")
+    lse2 = capi.DeviceBuffer((B, H, 1), "f32")
+    capi.attn_fwd(q, k, v, o2, lse2, cfg.scale, False)
+    capi.lib().sync()
+    od, ld = o.download(), lse.download()
+    _check("decode vs forward kernel O", od, o2.download(), TOL["bf16"])
+    _check("decode vs forward kernel LSE", ld, lse2.download()[..., 0], 1e-5)
+    qh = q.download()
+    # sampled heads: copy their K/V rows back (bh-contiguous slabs)
+    for (bb, hh) in [(0, 0), (33, 17), (63, 31)]:
+        bh = bb * H + hh
+        slab = Lkv * d
+        kb = np.empty(slab, np.uint16)
+        vb = np.empty(slab, np.uint16)
+        import ctypes as C
+        capi.lib().call("tt_memcpy_d2h", kb.ctypes.data, C.c_void_p(k.ptr + 2 * bh * slab), 2 * slab)
+        capi.lib().call("tt_memcpy_d2h", vb.ctypes.data, C.c_void_p(v.ptr + 2 * bh * slab), 2 * slab)
+        kh = capi.bf16_to_f32(kb).reshape(Lkv, d)
+        vh = capi.bf16_to_f32(vb).reshape(Lkv, d)
+        o_ref, l_ref = orc.attn_decode_f64(qh[bb, hh], kh, vh, cfg.scale)
+        _say(f" c4 head ({bb},{hh})")
+        _check("o", od[bb, hh], o_ref, TOL["bf16"])
+        _check("lse", ld[bb, hh], l_ref[0], TOL["bf16"])
+    assert abs(float(np.std(qh)) - 1.0) < 0.05  # the generator is N(0,1)
+
+
+# ------------------------------------------------------------------ shapes and edges
+
+SHAPES = [
+    # (B, H, Lq, Lk, d, causal)
+    (1, 1, 1, 1, 32, False),
+    (1, 2, 37, 37, 64, True),
+    (2, 1, 130, 130, 128, True),
+    (1, 3, 200, 77, 64, False),
+    (1, 1, 65, 300, 128, False),
+    (2, 2, 257, 257, 32, True),
+    (1, 1, 3, 1000, 64, False),
+]
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("shape", SHAPES, ids=[str(s) for s in SHAPES])
+def test_ragged_shapes(capi, dtype, shape):
+    B, H, Lq, Lk, d, causal = shape
+    _say(f"ragged {dtype} {shape}")
+    rng = np.random.default_rng(1000 + Lq + Lk + d)
+    x = {
+        "q": rng.standard_normal((B, H, Lq, d), dtype=np.float32),
+        "k": rng.standard_normal((B, H, Lk, d), dtype=np.float32),
+        "v": rng.standard_normal((B, H, Lk, d), dtype=np.float32),
+        "do": rng.standard_normal((B, H, Lq, d), dtype=np.float32),
+    }
+    if dtype == "bf16":
+        x = {n: orc.bf16_round(a) for n, a in x.items()}
+    scale = float(np.float32(1.0 / math.sqrt(d)))
+    tol = TOL["f32" if dtype == "f32" else "bf16"]
+    b = _run_fwd(capi, x, dtype, scale, causal)
+    o_ref, l_ref = orc.attn_fwd_f64(x["q"], x["k"], x["v"], scale, causal)
+    _check("O", b["o"].download(), o_ref, tol)
+    _check("LSE", b["lse"].download(), l_ref, tol)
+    dq, dk, dv = _run_bwd(capi, b, x["do"], dtype, scale, causal)
+    rq, rk, rv = orc.attn_bwd_f64(x["q"], x["k"], x["v"], x["do"], scale, causal)
+    _check("dQ", dq, rq, tol)
+    _check("dK", dk, rk, tol)
+    _check("dV", dv, rv, tol)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("Lkv,d", [(1, 64), (100, 32), (777, 128), (4096, 64), (5000, 128)])
+def test_decode_shapes(capi, dtype, Lkv, d):
+    _say(f"decode {dtype} Lkv={Lkv} d={d}")
+    rng = np.random.default_rng(Lkv + d)
+    B, H = 3, 5
+    q = rng.standard_normal((B, H, 1, d), dtype=np.float32)
+    k = rng.standard_normal((B, H, Lkv, d), dtype=np.float32)
+    v = rng.standard_normal((B, H, Lkv, d), dtype=np.float32)
+    if dtype == "bf16":
+        q, k, v = orc.bf16_round(q), orc.bf16_round(k), orc.bf16_round(v)
+    scale = float(np.float32(1.0 / math.sqrt(d)))
+    bq = capi.DeviceBuffer.from_numpy(q, dtype)
+    bk = capi.DeviceBuffer.from_numpy(k, dtype)
+    bv = capi.DeviceBuffer.from_numpy(v, dtype)
+    bo = capi.DeviceBuffer(q.shape, dtype)
+    bl = capi.DeviceBuffer((B, H), "f32")
+    capi.attn_decode(bq, bk, bv, bo, bl, scale)
+    o_ref, l_ref = orc.attn_decode_f64(q, k, v, scale)
+    tol = TOL["f32" if dtype == "f32" else "bf16"]
+    _check("o", bo.download(), o_ref, tol)
+    _check("lse", bl.download(), l_ref[..., 0], tol)
+
+
+def test_empty_inputs_are_noops(capi):
+    z = capi.DeviceBuffer((0, 2, 16, 64), "bf16")
+    capi.attn_fwd(z, z, z, z, None, 0.125, True)
+    e = capi.DeviceBuffer((1, 1, 0, 64), "f32")
+    capi.attn_fwd(e, e, e, e, None, 0.125, True)
+    # no queries: dK and dV are defined as zero
+    k = capi.DeviceBuffer.from_numpy(np.ones((1, 1, 5, 64), np.float32), "f32")
+    dk = capi.DeviceBuffer.from_numpy(np.full((1, 1, 5, 64), 7, np.float32), "f32")
+    dv = capi.DeviceBuffer.from_numpy(np.full((1, 1, 5, 64), 7, np.float32), "f32")
+    capi.attn_bwd(e, k, k, e, e, e, e, dk, dv, 0.125, False)
+    assert not dk.download().any() and not dv.download().any()
+
+
+def test_errors_are_reported(capi):
+    a = capi.DeviceBuffer((1, 1, 8, 96), "f32")
+    with pytest.raises(capi.TTError) as ei:
+        capi.attn_fwd(a, a, a, a, None, 0.1, False)
+    assert ei.value.code == capi.TT_ERR_UNSUPPORTED and "head dim" in str(ei.value)
+    q = capi.DeviceBuffer((1, 1, 8, 64), "f32")
+    k = capi.DeviceBuffer((1, 1, 9, 64), "f32")
+    with pytest.raises(capi.TTError) as ei:
+        capi.attn_fwd(q, k, k, q, None, 0.1, True)
+    assert ei.value.code == capi.TT_ERR_ARG and "Lq == Lk" in str(ei.value)
+    with pytest.raises(capi.TTError):
+        capi.lib().call("tt_attn_fwd_f32", None, None, None, None, None, 1, 1, 8, 8, 64, 0.1, 0, None)
+
+
+def orc_golden(name):
+    import os
+
+    return os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", name)
