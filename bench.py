@@ -1,0 +1,250 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X TinyTensor attention path (one GPU).
+
+Headline workload (BASELINE.json ``configs[4]``, the MFMA-utilisation
+config): causal attention forward + backward, bf16 inputs with fp32
+accumulation, B=4, H=32, L=4096, d=128.  One step = one forward
+(``tt_attn_fwd_bf16``) plus one backward (``tt_attn_bwd_bf16``) over inputs
+already resident in HBM.  ``value`` is the algorithmic rate in TFLOP/s:
+fwd = 4*B*H*L^2*d, bwd = 8*B*H*L^2*d (dV, dP, dQ, dK; recompute not counted),
+both halved by the causal mask -> 1.6493e12 FLOP per step.
+
+Second line item (``decode``): single-query decode, B=64, H=32, Lkv=8192,
+d=128, bf16, judged on HBM GB/s over K + V + q + o = 8,590,983,168 bytes.
+
+Per-kernel times come from HIP events recorded on the library stream right
+after each kernel launch (``tt_set_launch_events``) inside the timed region;
+``roofline`` is reported for the kernel with the largest share of the step.
+
+``cpu_baseline``: the reference's CPU path -- its op chain (Q @ K^T, * s,
++ mask, softmax by max/exp/sum/divide, @ V, and the backward by the same
+gradient rules) restated in float32 numpy by ``oracle/attn_oracle.py`` --
+timed on a bounded sample of the same workload's heads on the host cores.
+
+Prints ONE JSON line.  ``--gpus N`` with N > 1 exits: this build runs on one
+GPU (heads shard across GPUs without exchange; see the design notes).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "pku-aiprogramming_amd"))
+
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+
+C5 = dict(B=4, H=32, L=4096, d=128)
+C4 = dict(B=64, H=32, Lkv=8192, d=128)
+
+
+def fwdbwd_flops(B, H, L, d, causal=True):
+    f = 12.0 * B * H * L * L * d
+    return f / 2 if causal else f
+
+
+def kernel_flops(B, H, L, d):
+    """Algorithmic FLOPs each kernel of the step is charged with (causal)."""
+    u = 2.0 * B * H * L * L * d / 2  # one L x L x d GEMM under the causal mask
+    return {"attn_fwd": 2 * u, "attn_bwd_dkdv": 3 * u, "attn_bwd_dq": 1 * u, "attn_bwd_delta": 0.0}
+
+
+def decode_bytes(B, H, Lkv, d):
+    return 2 * (B * H * Lkv * d * 2) + 2 * (B * H * d * 2)
+
+
+def run_fwdbwd(T, steps, warmup):
+    B, H, L, d = C5["B"], C5["H"], C5["L"], C5["d"]
+    scale = float(__import__("numpy").float32(1.0 / math.sqrt(d)))
+    shp = (B, H, L, d)
+    q, k, v, do = (T.DeviceBuffer(shp, "bf16") for _ in range(4))
+    for i, b in enumerate((q, k, v, do)):
+        b.fill_normal(5000 + i)
+    o, dq, dk, dv = (T.DeviceBuffer(shp, "bf16") for _ in range(4))
+    lse = T.DeviceBuffer((B, H, L), "f32")
+
+    def step():
+        T.attn_fwd(q, k, v, o, lse, scale, True)
+        T.attn_bwd(q, k, v, o, lse, do, dq, dk, dv, scale, True)
+
+    for _ in range(warmup):
+        step()
+    T.lib().sync()
+
+    names = ["attn_fwd", "attn_bwd_delta", "attn_bwd_dkdv", "attn_bwd_dq"]
+    marks = [[T.Event() for _ in range(len(names) + 1)] for _ in range(steps)]
+    start, stop = T.Event(), T.Event()
+    T.lib().sync()
+    start.record()
+    for s in range(steps):
+        marks[s][0].record()
+        T.set_launch_events(marks[s][1:])
+        step()
+    stop.record()
+    T.lib().sync()
+    T.set_launch_events([])
+    total_ms = T.Event.elapsed(start, stop)
+    per = {n: 0.0 for n in names}
+    for s in range(steps):
+        for i, n in enumerate(names):
+            per[n] += T.Event.elapsed(marks[s][i], marks[s][i + 1])
+    per = {n: t / steps for n, t in per.items()}
+    return total_ms / steps, per
+
+
+def run_decode(T, steps, warmup):
+    B, H, Lkv, d = C4["B"], C4["H"], C4["Lkv"], C4["d"]
+    scale = float(__import__("numpy").float32(1.0 / math.sqrt(d)))
+    q = T.DeviceBuffer((B, H, 1, d), "bf16")
+    k = T.DeviceBuffer((B, H, Lkv, d), "bf16")
+    v = T.DeviceBuffer((B, H, Lkv, d), "bf16")
+    q.fill_normal(4000)
+    k.fill_normal(4001)
+    v.fill_normal(4002)
+    o = T.DeviceBuffer((B, H, 1, d), "bf16")
+    lse = T.DeviceBuffer((B, H), "f32")
+    for _ in range(warmup):
+        T.attn_decode(q, k, v, o, lse, scale)
+    T.lib().sync()
+    names = ["attn_decode_split", "attn_decode_combine"]
+    marks = [[T.Event() for _ in range(3)] for _ in range(steps)]
+    start, stop = T.Event(), T.Event()
+    start.record()
+    for s in range(steps):
+        marks[s][0].record()
+        T.set_launch_events(marks[s][1:])
+        T.attn_decode(q, k, v, o, lse, scale)
+    stop.record()
+    T.lib().sync()
+    T.set_launch_events([])
+    total_ms = T.Event.elapsed(start, stop)
+    per = {n: sum(T.Event.elapsed(marks[s][i], marks[s][i + 1]) for s in range(steps)) / steps
+           for i, n in enumerate(names)}
+    del k, v
+    return total_ms / steps, per
+
+
+def cpu_baseline(sample_heads):
+    """The reference's op chain in float32 numpy on `sample_heads` heads of
+    the headline workload (1 warm-up head, not counted)."""
+    import numpy as np
+
+    from oracle import attn_oracle as orc
+
+    try:
+        from threadpoolctl import threadpool_info
+
+        cores = max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
+    except Exception:
+        cores = os.cpu_count() or 1
+    L, d = C5["L"], C5["d"]
+    scale = float(np.float32(1.0 / math.sqrt(d)))
+    rng = np.random.default_rng(5)
+
+    def head():
+        return [orc.bf16_round(rng.standard_normal((L, d), dtype=np.float32)) for _ in range(4)]
+
+    q, k, v, do = head()
+    orc.composition_bwd_f32(q, k, v, do, scale, True)  # warm-up
+    t = 0.0
+    for _ in range(sample_heads):
+        q, k, v, do = head()
+        t0 = time.perf_counter()
+        orc.composition_bwd_f32(q, k, v, do, scale, True)  # forward (kept) + backward
+        t += time.perf_counter() - t0
+    flops = sample_heads * fwdbwd_flops(1, 1, L, d)
+    return {
+        "value": flops / t / 1e12,
+        "unit": "TFLOP/s",
+        "cores": int(cores),
+        "kind": "port",
+        "sample": f"{sample_heads} of the {C5['B'] * C5['H']} (b,h) heads of B=4 H=32 L=4096 d=128 causal "
+                  f"fwd+bwd, bf16-valued inputs in fp32, reference op order (full L x L materialised); "
+                  f"{t:.2f} s",
+    }
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--only", choices=["all", "fwdbwd", "decode"], default="all",
+                    help="run one workload only (for profiler runs)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-heads", type=int, default=128)
+    args = ap.parse_args(argv)
+
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              "(heads and batch shard across GPUs with no exchange, so N GPUs run N independent shares).",
+              file=sys.stderr)
+        return 2
+
+    import tt_capi as T
+
+    if T.lib().device_count() < 1:
+        print("bench.py: no HIP device visible", file=sys.stderr)
+        return 1
+
+    out = {
+        "metric": "attn fwd+bwd TFLOP/s (% bf16 MFMA peak); decode KV-read HBM GB/s (% peak)",
+        "value": None, "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": None, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic (on-device seeded N(0,1), bf16)",
+        "config": {"workload": "causal attention fwd+bwd, B=4 H=32 L=4096 d=128, bf16 in / fp32 accumulate",
+                   "B": C5["B"], "H": C5["H"], "L": C5["L"], "d": C5["d"], "causal": True,
+                   "flop_per_step": fwdbwd_flops(**C5)},
+    }
+
+    if args.only in ("all", "fwdbwd"):
+        ms, per = run_fwdbwd(T, args.steps, args.warmup)
+        flops = fwdbwd_flops(**C5)
+        out["ms_per_step"] = ms
+        out["value"] = flops / (ms * 1e-3) / 1e12
+        out["frac_of_peak"] = out["value"] / PEAK_BF16_TFLOPS
+        kf = kernel_flops(**C5)
+        kernels = {}
+        for n, t in per.items():
+            tf = kf[n] / (t * 1e-3) / 1e12 if kf[n] else None
+            kernels[n] = {"avg_ms": t, "tflops": tf, "frac": (tf / PEAK_BF16_TFLOPS) if tf else None}
+        out["kernels"] = kernels
+        dom = max(per, key=per.get)
+        ach = kf[dom] / (per[dom] * 1e-3) / 1e12
+        out["roofline"] = {"bound": "mfma", "kernel": dom, "achieved": ach, "peak": PEAK_BF16_TFLOPS,
+                           "unit": "TFLOP/s", "frac": ach / PEAK_BF16_TFLOPS, "traffic": None,
+                           "algorithmic_flop_per_launch": kf[dom]}
+
+    if args.only in ("all", "decode"):
+        ms, per = run_decode(T, args.steps, args.warmup)
+        nbytes = decode_bytes(**C4)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        split = per["attn_decode_split"]
+        split_bytes = nbytes - C4["B"] * C4["H"] * C4["d"] * 2  # o is written by the combine kernel
+        sgbs = split_bytes / (split * 1e-3) / 1e9
+        out["decode"] = {
+            "workload": "decode B=64 H=32 Lkv=8192 d=128 bf16", "value": gbs, "unit": "GB/s",
+            "ms_per_step": ms, "frac_of_peak": gbs / PEAK_HBM_GBS, "bytes_per_step": nbytes,
+            "kernels": {n: {"avg_ms": t} for n, t in per.items()},
+            "roofline": {"bound": "hbm", "kernel": "attn_decode_split", "achieved": sgbs, "peak": PEAK_HBM_GBS,
+                         "unit": "GB/s", "frac": sgbs / PEAK_HBM_GBS, "traffic": None,
+                         "algorithmic_bytes_per_launch": split_bytes},
+        }
+        if args.only == "decode":
+            out["value"], out["unit"], out["ms_per_step"] = gbs, "GB/s", ms
+            out["roofline"] = out["decode"]["roofline"]
+
+    if not args.no_cpu_baseline and args.cpu_heads > 0:
+        out["cpu_baseline"] = cpu_baseline(args.cpu_heads)
+
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

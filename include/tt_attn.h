@@ -86,6 +86,12 @@ int tt_event_record(void* ev, void* stream);
 int tt_event_elapsed_ms(float* ms, void* start, void* stop);
 int tt_event_destroy(void* ev);
 
+/* Benchmark instrumentation (no counterpart in the reference): after this
+ * call the library records evs[i] on the launch stream right after its i-th
+ * kernel launch, for i < n; later launches record nothing.  n = 0 (or
+ * evs = NULL) disables it.  The events must stay alive until recorded. */
+int tt_set_launch_events(void** evs, int n);
+
 /* ------------------------------------------------------------ elementwise */
 
 /* Elementwise ops of TinyTensor (src/TinyTensor_kernels.cu:6-85).

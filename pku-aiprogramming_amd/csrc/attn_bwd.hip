@@ -585,7 +585,7 @@ static int launch_bwd(const T* q, const T* k, const T* v, const T* o, const floa
   const int64_t dblk = (rows + (256 / TPR) - 1) / (256 / TPR);
   if (dblk > 0x7fffffff) return fail(TT_ERR_ARG, "attention backward: grid too large");
   hipLaunchKernelGGL((attn_bwd_delta_kernel<T, D>), dim3((unsigned)dblk), dim3(256), 0, st, o, dout, delta, rows);
-  TT_LAUNCH_CHECK("attention backward delta launch");
+  TT_LAUNCHED("attention backward delta launch", st);
 
   const float sl2 = scale * kLog2e;
   const int64_t nkt = (Lk + DKDV_BN - 1) / DKDV_BN;
@@ -595,17 +595,17 @@ static int launch_bwd(const T* q, const T* k, const T* v, const T* o, const floa
   if constexpr (BF) {
     hipLaunchKernelGGL((attn_bwd_dkdv_bf16_kernel<D, CAUSAL>), dim3((unsigned)(nkt * BH)), dim3(256), 0, st,
                        q, k, v, dout, lse, delta, dk, dv, (int)Lq, (int)Lk, (int)BH, (int)nkt, gk, sl2, scale);
-    TT_LAUNCH_CHECK("attention backward dK/dV launch");
+    TT_LAUNCHED("attention backward dK/dV launch", st);
     hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<D, CAUSAL>), dim3((unsigned)(nqt * BH)), dim3(256), 0, st,
                        q, k, v, dout, lse, delta, dq, (int)Lq, (int)Lk, (int)BH, (int)nqt, gq, sl2, scale);
-    TT_LAUNCH_CHECK("attention backward dQ launch");
+    TT_LAUNCHED("attention backward dQ launch", st);
   } else {
     hipLaunchKernelGGL((attn_bwd_dkdv_f32_kernel<D, CAUSAL>), dim3((unsigned)(nkt * BH)), dim3(256), 0, st,
                        q, k, v, dout, lse, delta, dk, dv, (int)Lq, (int)Lk, (int)BH, (int)nkt, gk, sl2, scale);
-    TT_LAUNCH_CHECK("attention backward dK/dV launch");
+    TT_LAUNCHED("attention backward dK/dV launch", st);
     hipLaunchKernelGGL((attn_bwd_dq_f32_kernel<D, CAUSAL>), dim3((unsigned)(nqt * BH)), dim3(256), 0, st,
                        q, k, v, dout, lse, delta, dq, (int)Lq, (int)Lk, (int)BH, (int)nqt, gq, sl2, scale);
-    TT_LAUNCH_CHECK("attention backward dQ launch");
+    TT_LAUNCHED("attention backward dQ launch", st);
   }
   return ok();
 }

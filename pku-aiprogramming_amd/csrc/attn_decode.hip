@@ -204,10 +204,10 @@ static int launch_decode(const T* q, const T* k, const T* v, T* o, float* lse, i
   hipLaunchKernelGGL((attn_decode_split_kernel<T, D, 8>), dim3((unsigned)(nsplit * BH)),
                      dim3(DEC_THREADS), 0, st, q, k, v, part_o, part_lse, (int)Lkv, (int)nsplit, chunk,
                      scale * kLog2e);
-  TT_LAUNCH_CHECK("attention decode split launch");
+  TT_LAUNCHED("attention decode split launch", st);
   hipLaunchKernelGGL((attn_decode_combine_kernel<T, D>), dim3((unsigned)BH), dim3(D), 0, st, part_o,
                      part_lse, o, lse, (int)nsplit);
-  TT_LAUNCH_CHECK("attention decode combine launch");
+  TT_LAUNCHED("attention decode combine launch", st);
   return ok();
 }
 

@@ -316,7 +316,7 @@ static int launch_fwd(KernelPtr kern, const T* q, const T* k, const T* v, T* o, 
   const int group = pick_group(BH, nqt, 64);
   hipLaunchKernelGGL(kern, dim3((unsigned)nblk), dim3(256), 0, s, q, k, v, o, lse, (int)Lq, (int)Lk,
                      (int)BH, (int)nqt, group, scale * kLog2e);
-  TT_LAUNCH_CHECK("attention forward launch");
+  TT_LAUNCHED("attention forward launch", s);
   return ok();
 }
 

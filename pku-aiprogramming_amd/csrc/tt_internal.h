@@ -22,6 +22,10 @@ int hip_fail(hipError_t e, const char* what);
 hipStream_t stream_or_default(void* s);
 int ensure_init();
 
+// Records the next instrumentation event (tt_set_launch_events) after a
+// kernel launch on `s`; a no-op unless instrumentation is enabled.
+void after_launch(hipStream_t s);
+
 // Device scratch owned by the library, grown on demand and kept for reuse.
 // `slot` separates independent users (0: attention bwd row sums,
 // 1: decode partials).  Stream-ordered on the library stream; callers that
@@ -40,4 +44,11 @@ int workspace(int slot, size_t bytes, void** ptr);
   do {                                                         \
     hipError_t e_ = hipGetLastError();                         \
     if (e_ != hipSuccess) return tt::hip_fail(e_, what);       \
+  } while (0)
+
+// Launch-error check plus the instrumentation hook, for kernels on stream s.
+#define TT_LAUNCHED(what, s)    \
+  do {                          \
+    TT_LAUNCH_CHECK(what);      \
+    tt::after_launch(s);        \
   } while (0)

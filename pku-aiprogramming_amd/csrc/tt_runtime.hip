@@ -13,6 +13,7 @@
 #include <mutex>
 #include <string>
 #include <unordered_map>
+#include <vector>
 
 #include "tt_internal.h"
 
@@ -100,6 +101,15 @@ static int alloc_block(size_t bytes, void** ptr) {
   g_alloc.in_use += cls;
   *ptr = p;
   return TT_OK;
+}
+
+// ---------------------------------------------------------------- instrumentation
+static std::vector<void*> g_launch_events;
+static size_t g_launch_next = 0;
+
+void after_launch(hipStream_t s) {
+  if (g_launch_next >= g_launch_events.size()) return;
+  (void)hipEventRecord((hipEvent_t)g_launch_events[g_launch_next++], s);
 }
 
 // ---------------------------------------------------------------- workspace
@@ -395,6 +405,13 @@ int tt_event_destroy(void* ev) {
   if (!ev) return TT_OK;
   TT_HIP(hipEventDestroy((hipEvent_t)ev));
   return ok();
+}
+
+int tt_set_launch_events(void** evs, int n) {
+  g_launch_events.clear();
+  g_launch_next = 0;
+  if (evs && n > 0) g_launch_events.assign(evs, evs + n);
+  return TT_OK;
 }
 
 int tt_elementwise(int op, int dtype, void* c, const void* a, const void* b, int64_t n,

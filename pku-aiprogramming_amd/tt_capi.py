@@ -45,6 +45,7 @@ _SIGS = {
     "tt_event_record": (C.c_int, [_p, _p]),
     "tt_event_elapsed_ms": (C.c_int, [C.POINTER(C.c_float), _p, _p]),
     "tt_event_destroy": (C.c_int, [_p]),
+    "tt_set_launch_events": (C.c_int, [C.POINTER(_p), C.c_int]),
     "tt_elementwise": (C.c_int, [C.c_int, C.c_int, _p, _p, _p, _i64, C.c_double, C.c_double, C.c_uint64, _p]),
     "tt_fill_normal": (C.c_int, [C.c_int, _p, _i64, C.c_uint64, C.c_float, _p]),
     "tt_attn_fwd_f32": (C.c_int, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, C.c_float, C.c_int, _p]),
@@ -211,6 +212,38 @@ def attn_decode(q, k, v, o, lse, scale: float, stream=None):
     Lkv = k.shape[2]
     name = "tt_attn_decode_bf16" if q.dtype == "bf16" else "tt_attn_decode_f32"
     lib().call(name, q.ptr, k.ptr, v.ptr, o.ptr, lse.ptr if lse else None, B, H, Lkv, d, scale, stream)
+
+
+class Event:
+    """One hipEvent; ``elapsed(a, b)`` reads the time between two of them."""
+
+    def __init__(self):
+        self.L = lib()
+        e = C.c_void_p()
+        self.L.call("tt_event_create", C.byref(e))
+        self.ptr = e.value
+
+    def record(self, stream=None):
+        self.L.call("tt_event_record", self.ptr, stream)
+
+    @staticmethod
+    def elapsed(a: "Event", b: "Event") -> float:
+        ms = C.c_float(0)
+        lib().call("tt_event_elapsed_ms", C.byref(ms), a.ptr, b.ptr)
+        return ms.value
+
+    def __del__(self):
+        try:
+            self.L.lib.tt_event_destroy(self.ptr)
+        except Exception:
+            pass
+
+
+def set_launch_events(events: Sequence[Event]):
+    """Record events[i] after the library's i-th next kernel launch
+    (instrumentation for per-kernel timing); [] disables it."""
+    arr = (C.c_void_p * max(1, len(events)))(*[e.ptr for e in events])
+    lib().call("tt_set_launch_events", arr, len(events))
 
 
 class Timer:
