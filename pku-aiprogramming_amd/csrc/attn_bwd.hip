@@ -13,15 +13,20 @@
 //
 // Two kernels split the work so that every output row has one owner and no
 // atomics are needed:
-//   dkdv: workgroup = 128 keys (32 per wave, lane = key); loops over query
-//         tiles of 64 staged in LDS both row-major (S, dP operands) and
-//         transposed (dV^T += dO^T P, dK^T += Q^T dS operands).
+//   dkdv: workgroup = 128 keys (32 per wave, lane = key, K/V rows held in
+//         registers); loops over query tiles of 64 staged once in LDS.  The
+//         same LDS tile feeds the S / dP operands (16-byte row reads) and the
+//         transposed dV^T += dO^T P, dK^T += Q^T dS operands (gfx950
+//         transpose reads), so nothing is transposed on the way in.
 //   dq:   workgroup = 128 queries (lane = query, as in the forward); loops over
-//         key tiles of 64 staged row-major (S^T, dP^T) and transposed
-//         (dQ^T += K^T dS^T).
+//         key tiles of 64: S^T and dP^T from K / V row reads, dQ^T += K^T dS^T
+//         from transpose reads of the same K tile.
+// Loads past the end of a sequence read a clamped (valid) row and the
+// result is masked, so the inner loops carry no load guards.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
+#include <type_traits>
 
 #include "attn_common.h"
 #include "attn_tiles.h"
@@ -71,15 +76,12 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_bf16_kernel(
     const u16* __restrict__ dO, const float* __restrict__ LSE, const float* __restrict__ Delta,
     u16* __restrict__ dK, u16* __restrict__ dV, int Lq, int Lk, int BH, int nkt, int group, float sl2,
     float scale) {
+  using Tile = SwzTile<D>;
   constexpr int BN = DKDV_BN, BQ = DKDV_BQ;
-  constexpr int RP = D + 8;   // row-major pitch
-  constexpr int TP = BQ + 8;  // transposed pitch
   constexpr int NC = D / 16, ND = D / 32, CPR = D / 8;
   constexpr int LPT = BQ * CPR / 256;
-  __shared__ __align__(16) u16 sQ[BQ * RP];
-  __shared__ __align__(16) u16 sdO[BQ * RP];
-  __shared__ __align__(16) u16 sQt[D * TP];
-  __shared__ __align__(16) u16 sdOt[D * TP];
+  __shared__ __align__(16) u16 sQ[Tile::kElems(BQ)];
+  __shared__ __align__(16) u16 sdO[Tile::kElems(BQ)];
   __shared__ __align__(16) float sL[BQ];
   __shared__ __align__(16) float sDl[BQ];
 
@@ -94,19 +96,22 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_bf16_kernel(
   const int64_t lbase = (int64_t)bh * Lq;
 
   bf16x8 kf[NC], vf[NC];
+  {
+    const int kr = min(key, Lk - 1);  // rows past Lk compute garbage that is never stored
 #pragma unroll
-  for (int c = 0; c < NC; ++c) {
-    uint4 a = {0, 0, 0, 0}, b = {0, 0, 0, 0};
-    if (key < Lk) {
-      a = ldg16(K + kbase + (int64_t)key * D + 16 * c + 8 * g);
-      b = ldg16(V + kbase + (int64_t)key * D + 16 * c + 8 * g);
+    for (int c = 0; c < NC; ++c) {
+      kf[c] = __builtin_bit_cast(bf16x8, ldg16(K + kbase + (int64_t)kr * D + 16 * c + 8 * g));
+      vf[c] = __builtin_bit_cast(bf16x8, ldg16(V + kbase + (int64_t)kr * D + 16 * c + 8 * g));
     }
-    kf[c] = *reinterpret_cast<bf16x8*>(&a);
-    vf[c] = *reinterpret_cast<bf16x8*>(&b);
   }
   f32x16 adk[ND], adv[ND];
 #pragma unroll
   for (int dt = 0; dt < ND; ++dt) adk[dt] = adv[dt] = f32x16{};
+
+  // transpose-read addressing (this lane as a source row/column)
+  const int t16 = l & 15;
+  const int trow = 4 * g + (t16 >> 2);
+  const int tcol = 16 * ((l >> 4) & 1) + 4 * (t16 & 3);
 
   uint4 qreg[LPT], oreg[LPT];
   float lreg = 0.f, dreg = 0.f;
@@ -114,11 +119,9 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_bf16_kernel(
 #pragma unroll
     for (int i = 0; i < LPT; ++i) {
       const int c = tid + 256 * i;
-      const int row = c % BQ, ch = c / BQ;  // row-fastest: conflict-free transposed stores
-      uint4 z = {0, 0, 0, 0};
-      const bool in = qb + row < Lq;
-      qreg[i] = in ? ldg16(Q + qbase + (int64_t)(qb + row) * D + 8 * ch) : z;
-      oreg[i] = in ? ldg16(dO + qbase + (int64_t)(qb + row) * D + 8 * ch) : z;
+      const int row = min(qb + c / CPR, Lq - 1), ch = c % CPR;
+      qreg[i] = ldg16(Q + qbase + (int64_t)row * D + 8 * ch);
+      oreg[i] = ldg16(dO + qbase + (int64_t)row * D + 8 * ch);
     }
     if (tid < BQ) {
       const bool in = qb + tid < Lq;
@@ -130,17 +133,9 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_bf16_kernel(
 #pragma unroll
     for (int i = 0; i < LPT; ++i) {
       const int c = tid + 256 * i;
-      const int row = c % BQ, ch = c / BQ;
-      *reinterpret_cast<uint4*>(&sQ[row * RP + 8 * ch]) = qreg[i];
-      *reinterpret_cast<uint4*>(&sdO[row * RP + 8 * ch]) = oreg[i];
-      const u16* eq = reinterpret_cast<const u16*>(&qreg[i]);
-      const u16* eo = reinterpret_cast<const u16*>(&oreg[i]);
-      const int pos = perm16(row);
-#pragma unroll
-      for (int x = 0; x < 8; ++x) {
-        sQt[(8 * ch + x) * TP + pos] = eq[x];
-        sdOt[(8 * ch + x) * TP + pos] = eo[x];
-      }
+      const int row = c / CPR, ch = c % CPR;
+      *reinterpret_cast<uint4*>(&sQ[Tile::chunk(row, ch)]) = qreg[i];
+      *reinterpret_cast<uint4*>(&sdO[Tile::chunk(row, ch)]) = oreg[i];
     }
     if (tid < BQ) {
       sL[tid] = lreg;
@@ -148,30 +143,18 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_bf16_kernel(
     }
   };
 
-  const int qstart = CAUSAL ? (k0 / BQ) * BQ : 0;
-  if (qstart < Lq) gload(qstart);
-  for (int qb = qstart; qb < Lq; qb += BQ) {
-    __syncthreads();
-    sstore();
-    __syncthreads();
-    if (qb + BQ < Lq) gload(qb + BQ);
-    if (CAUSAL && qb + BQ - 1 < wk_lo) continue;  // every query of the tile precedes every key of the wave
-
+  auto step = [&](int qb, auto mask_tag) {
+    constexpr bool MASK = decltype(mask_tag)::value;
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
       f32x16 s = f32x16{}, dp = f32x16{};
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
-        bf16x8 a = *reinterpret_cast<const bf16x8*>(&sQ[(32 * mt + r32) * RP + 16 * c + 8 * g]);
-        s = mfma_bf16_32x32x16(a, kf[c], s);
-      }
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        bf16x8 a = *reinterpret_cast<const bf16x8*>(&sdO[(32 * mt + r32) * RP + 16 * c + 8 * g]);
-        dp = mfma_bf16_32x32x16(a, vf[c], dp);
+        const int off = Tile::chunk(32 * mt + r32, 2 * c + g);
+        s = mfma_bf16_32x32x16(*reinterpret_cast<const bf16x8*>(&sQ[off]), kf[c], s);
+        dp = mfma_bf16_32x32x16(*reinterpret_cast<const bf16x8*>(&sdO[off]), vf[c], dp);
       }
       // s[r] = S[query qb + 32mt + acc_row(r, g)][key]
-      const bool need_mask = CAUSAL && (qb + 32 * mt < wk_lo + 31);
       bf16x8 pb[2], db[2];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -183,24 +166,39 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_bf16_kernel(
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
           const int r = 4 * j + u;
-          float p = fast_exp2(s[r] * sl2 - la[u]);
-          if (need_mask && key > qb + qi + u) p = 0.f;
-          const float ds = p * (dp[r] - da[u]);
+          float p = fast_exp2(fmaf(s[r], sl2, -la[u]));
+          if constexpr (MASK)
+            if (key > qb + qi + u) p = 0.f;
           pb[r >> 3][r & 7] = (__bf16)p;
-          db[r >> 3][r & 7] = (__bf16)ds;
+          db[r >> 3][r & 7] = (__bf16)(p * (dp[r] - da[u]));
         }
       }
+      // dV^T += dO^T P and dK^T += Q^T dS over the 32 queries of this half:
+      // k-chunk h holds queries 32mt + 16h + perm16 order.
 #pragma unroll
-      for (int dt = 0; dt < ND; ++dt)
+      for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const int off = (32 * dt + r32) * TP + 16 * (2 * mt + h) + 8 * g;
-          bf16x8 ao = *reinterpret_cast<const bf16x8*>(&sdOt[off]);
-          adv[dt] = mfma_bf16_32x32x16(ao, pb[h], adv[dt]);
-          bf16x8 aq = *reinterpret_cast<const bf16x8*>(&sQt[off]);
-          adk[dt] = mfma_bf16_32x32x16(aq, db[h], adk[dt]);
+        for (int dt = 0; dt < ND; ++dt) {
+          const int r0 = 32 * mt + 16 * h + trow;
+          const int o0 = Tile::at4(r0, 32 * dt + tcol), o1 = Tile::at4(r0 + 8, 32 * dt + tcol);
+          adv[dt] = mfma_bf16_32x32x16(lds_read_tr16x2(&sdO[o0], &sdO[o1]), pb[h], adv[dt]);
+          adk[dt] = mfma_bf16_32x32x16(lds_read_tr16x2(&sQ[o0], &sQ[o1]), db[h], adk[dt]);
         }
     }
+  };
+
+  const int qstart = CAUSAL ? (k0 / BQ) * BQ : 0;
+  if (qstart < Lq) gload(qstart);
+  for (int qb = qstart; qb < Lq; qb += BQ) {
+    __syncthreads();
+    sstore();
+    __syncthreads();
+    if (qb + BQ < Lq) gload(qb + BQ);
+    if (CAUSAL && qb + BQ - 1 < wk_lo) continue;  // every query of the tile precedes every key of the wave
+    if (CAUSAL && qb < wk_lo + 31)
+      step(qb, std::true_type{});
+    else
+      step(qb, std::false_type{});
   }
 
   if (key < Lk) {
@@ -224,17 +222,17 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_bf16_kernel(
 
 // ------------------------------------------------------------------ bf16 dQ
 template <int D, bool CAUSAL>
-__global__ __launch_bounds__(256, 1) void attn_bwd_dq_bf16_kernel(
+__global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void attn_bwd_dq_bf16_kernel(
     const u16* __restrict__ Q, const u16* __restrict__ K, const u16* __restrict__ V,
     const u16* __restrict__ dO, const float* __restrict__ LSE, const float* __restrict__ Delta,
     u16* __restrict__ dQ, int Lq, int Lk, int BH, int nqt, int group, float sl2, float scale) {
+  using Tile = SwzTile<D>;
   constexpr int BM = DQ_BM, BN = DQ_BN;
-  constexpr int RP = D + 8, TP = BN + 8;
+  constexpr int VP = D + 8;
   constexpr int NC = D / 16, ND = D / 32, CPR = D / 8;
   constexpr int LPT = BN * CPR / 256;
-  __shared__ __align__(16) u16 sK[BN * RP];
-  __shared__ __align__(16) u16 sV[BN * RP];
-  __shared__ __align__(16) u16 sKt[D * TP];
+  __shared__ __align__(16) u16 sK[Tile::kElems(BN)];
+  __shared__ __align__(16) u16 sV[BN * VP];
 
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, g = l >> 5, r32 = l & 31;
   int qt, bh;
@@ -246,15 +244,13 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_bf16_kernel(
   const int64_t kbase = (int64_t)bh * Lk * D;
 
   bf16x8 qf[NC], dof[NC];
+  {
+    const int qr = min(qrow, Lq - 1);
 #pragma unroll
-  for (int c = 0; c < NC; ++c) {
-    uint4 a = {0, 0, 0, 0}, b = {0, 0, 0, 0};
-    if (qrow < Lq) {
-      a = ldg16(Q + qbase + (int64_t)qrow * D + 16 * c + 8 * g);
-      b = ldg16(dO + qbase + (int64_t)qrow * D + 16 * c + 8 * g);
+    for (int c = 0; c < NC; ++c) {
+      qf[c] = __builtin_bit_cast(bf16x8, ldg16(Q + qbase + (int64_t)qr * D + 16 * c + 8 * g));
+      dof[c] = __builtin_bit_cast(bf16x8, ldg16(dO + qbase + (int64_t)qr * D + 16 * c + 8 * g));
     }
-    qf[c] = *reinterpret_cast<bf16x8*>(&a);
-    dof[c] = *reinterpret_cast<bf16x8*>(&b);
   }
   const float lse2 = qrow < Lq ? LSE[(int64_t)bh * Lq + qrow] * kLog2e : INFINITY;
   const float dl = qrow < Lq ? Delta[(int64_t)bh * Lq + qrow] : 0.f;
@@ -262,29 +258,60 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_bf16_kernel(
 #pragma unroll
   for (int dt = 0; dt < ND; ++dt) adq[dt] = f32x16{};
 
+  const int t16 = l & 15;
+  const int trow = 4 * g + (t16 >> 2);
+  const int tcol = 16 * ((l >> 4) & 1) + 4 * (t16 & 3);
+
   uint4 kreg[LPT], vreg[LPT];
   auto gload = [&](int kb) {
 #pragma unroll
     for (int i = 0; i < LPT; ++i) {
       const int c = tid + 256 * i;
-      const int key = c % BN, ch = c / BN;
-      uint4 z = {0, 0, 0, 0};
-      const bool in = kb + key < Lk;
-      kreg[i] = in ? ldg16(K + kbase + (int64_t)(kb + key) * D + 8 * ch) : z;
-      vreg[i] = in ? ldg16(V + kbase + (int64_t)(kb + key) * D + 8 * ch) : z;
+      const int row = min(kb + c / CPR, Lk - 1), ch = c % CPR;
+      kreg[i] = ldg16(K + kbase + (int64_t)row * D + 8 * ch);
+      vreg[i] = ldg16(V + kbase + (int64_t)row * D + 8 * ch);
     }
   };
   auto sstore = [&]() {
 #pragma unroll
     for (int i = 0; i < LPT; ++i) {
       const int c = tid + 256 * i;
-      const int key = c % BN, ch = c / BN;
-      *reinterpret_cast<uint4*>(&sK[key * RP + 8 * ch]) = kreg[i];
-      *reinterpret_cast<uint4*>(&sV[key * RP + 8 * ch]) = vreg[i];
-      const u16* ek = reinterpret_cast<const u16*>(&kreg[i]);
-      const int pos = perm16(key);
+      const int row = c / CPR, ch = c % CPR;
+      *reinterpret_cast<uint4*>(&sK[Tile::chunk(row, ch)]) = kreg[i];
+      *reinterpret_cast<uint4*>(&sV[row * VP + 8 * ch]) = vreg[i];
+    }
+  };
+
+  auto tile = [&](int kb, auto mask_tag) {
+    constexpr bool MASK = decltype(mask_tag)::value;
 #pragma unroll
-      for (int x = 0; x < 8; ++x) sKt[(8 * ch + x) * TP + pos] = ek[x];
+    for (int t = 0; t < 2; ++t) {
+      f32x16 s = f32x16{}, dp = f32x16{};
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const bf16x8 a = *reinterpret_cast<const bf16x8*>(&sK[Tile::chunk(32 * t + r32, 2 * c + g)]);
+        s = mfma_bf16_32x32x16(a, qf[c], s);
+        const bf16x8 b = *reinterpret_cast<const bf16x8*>(&sV[(32 * t + r32) * VP + 16 * c + 8 * g]);
+        dp = mfma_bf16_32x32x16(b, dof[c], dp);
+      }
+      bf16x8 db[2];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float p = fast_exp2(fmaf(s[r], sl2, -lse2));
+        if constexpr (MASK) {
+          const int kk = kb + 32 * t + acc_row(r, g);
+          if (kk >= Lk || (CAUSAL && kk > qrow)) p = 0.f;
+        }
+        db[r >> 3][r & 7] = (__bf16)(p * (dp[r] - dl));
+      }
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int dt = 0; dt < ND; ++dt) {
+          const int r0 = 32 * t + 16 * h + trow;
+          const bf16x8 a = lds_read_tr16x2(&sK[Tile::at4(r0, 32 * dt + tcol)], &sK[Tile::at4(r0 + 8, 32 * dt + tcol)]);
+          adq[dt] = mfma_bf16_32x32x16(a, db[h], adq[dt]);
+        }
     }
   };
 
@@ -296,38 +323,10 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_bf16_kernel(
     __syncthreads();
     if (kb + BN < kend) gload(kb + BN);
     if (CAUSAL && kb > wq_hi) continue;
-    const bool need_mask = (kb + BN > Lk) || (CAUSAL && kb + BN - 1 > wq_lo);
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      f32x16 s = f32x16{}, dp = f32x16{};
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        bf16x8 a = *reinterpret_cast<const bf16x8*>(&sK[(32 * t + r32) * RP + 16 * c + 8 * g]);
-        s = mfma_bf16_32x32x16(a, qf[c], s);
-      }
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        bf16x8 a = *reinterpret_cast<const bf16x8*>(&sV[(32 * t + r32) * RP + 16 * c + 8 * g]);
-        dp = mfma_bf16_32x32x16(a, dof[c], dp);
-      }
-      bf16x8 db[2];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float p = fast_exp2(s[r] * sl2 - lse2);
-        if (need_mask) {
-          const int kk = kb + 32 * t + acc_row(r, g);
-          if (kk >= Lk || (CAUSAL && kk > qrow)) p = 0.f;
-        }
-        db[r >> 3][r & 7] = (__bf16)(p * (dp[r] - dl));
-      }
-#pragma unroll
-      for (int dt = 0; dt < ND; ++dt)
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          bf16x8 a = *reinterpret_cast<const bf16x8*>(&sKt[(32 * dt + r32) * TP + 16 * (2 * t + h) + 8 * g]);
-          adq[dt] = mfma_bf16_32x32x16(a, db[h], adq[dt]);
-        }
-    }
+    if ((kb + BN > Lk) || (CAUSAL && kb + BN - 1 > wq_lo))
+      tile(kb, std::true_type{});
+    else
+      tile(kb, std::false_type{});
   }
 
   if (qrow < Lq) {
@@ -345,6 +344,9 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_bf16_kernel(
 }
 
 // ------------------------------------------------------------------ fp32 dK, dV
+// Same schedule on v_mfma_f32_32x32x2f32.  Each fp32 MFMA takes one k-value
+// per lane half, so the transposed operands are plain column reads of the
+// row-major tiles (consecutive lanes, consecutive columns).
 template <int D, bool CAUSAL>
 __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_f32_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
@@ -371,10 +373,13 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_f32_kernel(
   const int64_t lbase = (int64_t)bh * Lq;
 
   float kf[NC], vf[NC];
+  {
+    const int kr = min(key, Lk - 1);
 #pragma unroll
-  for (int c = 0; c < NC; ++c) {
-    kf[c] = key < Lk ? K[kbase + (int64_t)key * D + 2 * c + g] : 0.f;
-    vf[c] = key < Lk ? V[kbase + (int64_t)key * D + 2 * c + g] : 0.f;
+    for (int c = 0; c < NC; ++c) {
+      kf[c] = K[kbase + (int64_t)kr * D + 2 * c + g];
+      vf[c] = V[kbase + (int64_t)kr * D + 2 * c + g];
+    }
   }
   f32x16 adk[ND], adv[ND];
 #pragma unroll
@@ -386,11 +391,9 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_f32_kernel(
 #pragma unroll
     for (int i = 0; i < LPT; ++i) {
       const int c = tid + 256 * i;
-      const int row = c / CPR, ch = c % CPR;
-      float4 z = {0.f, 0.f, 0.f, 0.f};
-      const bool in = qb + row < Lq;
-      qreg[i] = in ? *reinterpret_cast<const float4*>(Q + qbase + (int64_t)(qb + row) * D + 4 * ch) : z;
-      oreg[i] = in ? *reinterpret_cast<const float4*>(dO + qbase + (int64_t)(qb + row) * D + 4 * ch) : z;
+      const int row = min(qb + c / CPR, Lq - 1), ch = c % CPR;
+      qreg[i] = *reinterpret_cast<const float4*>(Q + qbase + (int64_t)row * D + 4 * ch);
+      oreg[i] = *reinterpret_cast<const float4*>(dO + qbase + (int64_t)row * D + 4 * ch);
     }
     if (tid < BQ) {
       const bool in = qb + tid < Lq;
@@ -435,7 +438,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_f32_kernel(
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int qi = 32 * mt + acc_row(r, g);
-        float p = fast_exp2(s[r] * sl2 - sL[qi]);
+        float p = fast_exp2(fmaf(s[r], sl2, -sL[qi]));
         if (need_mask && key > qb + qi) p = 0.f;
         pr[r] = p;
         dsr[r] = p * (dp[r] - sDl[qi]);
@@ -490,10 +493,13 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_f32_kernel(
   const int64_t kbase = (int64_t)bh * Lk * D;
 
   float qf[NC], dof[NC];
+  {
+    const int qr = min(qrow, Lq - 1);
 #pragma unroll
-  for (int c = 0; c < NC; ++c) {
-    qf[c] = qrow < Lq ? Q[qbase + (int64_t)qrow * D + 2 * c + g] : 0.f;
-    dof[c] = qrow < Lq ? dO[qbase + (int64_t)qrow * D + 2 * c + g] : 0.f;
+    for (int c = 0; c < NC; ++c) {
+      qf[c] = Q[qbase + (int64_t)qr * D + 2 * c + g];
+      dof[c] = dO[qbase + (int64_t)qr * D + 2 * c + g];
+    }
   }
   const float lse2 = qrow < Lq ? LSE[(int64_t)bh * Lq + qrow] * kLog2e : INFINITY;
   const float dl = qrow < Lq ? Delta[(int64_t)bh * Lq + qrow] : 0.f;
@@ -506,20 +512,18 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_f32_kernel(
 #pragma unroll
     for (int i = 0; i < LPT; ++i) {
       const int c = tid + 256 * i;
-      const int key = c / CPR, ch = c % CPR;
-      float4 z = {0.f, 0.f, 0.f, 0.f};
-      const bool in = kb + key < Lk;
-      kreg[i] = in ? *reinterpret_cast<const float4*>(K + kbase + (int64_t)(kb + key) * D + 4 * ch) : z;
-      vreg[i] = in ? *reinterpret_cast<const float4*>(V + kbase + (int64_t)(kb + key) * D + 4 * ch) : z;
+      const int row = min(kb + c / CPR, Lk - 1), ch = c % CPR;
+      kreg[i] = *reinterpret_cast<const float4*>(K + kbase + (int64_t)row * D + 4 * ch);
+      vreg[i] = *reinterpret_cast<const float4*>(V + kbase + (int64_t)row * D + 4 * ch);
     }
   };
   auto sstore = [&]() {
 #pragma unroll
     for (int i = 0; i < LPT; ++i) {
       const int c = tid + 256 * i;
-      const int key = c / CPR, ch = c % CPR;
-      float* pk = &sK[key * P + 4 * ch];
-      float* pv = &sV[key * P + 4 * ch];
+      const int row = c / CPR, ch = c % CPR;
+      float* pk = &sK[row * P + 4 * ch];
+      float* pv = &sV[row * P + 4 * ch];
       pk[0] = kreg[i].x; pk[1] = kreg[i].y; pk[2] = kreg[i].z; pk[3] = kreg[i].w;
       pv[0] = vreg[i].x; pv[1] = vreg[i].y; pv[2] = vreg[i].z; pv[3] = vreg[i].w;
     }
@@ -545,7 +549,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_f32_kernel(
       float dsr[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        float p = fast_exp2(s[r] * sl2 - lse2);
+        float p = fast_exp2(fmaf(s[r], sl2, -lse2));
         if (need_mask) {
           const int kk = kb + 32 * t + acc_row(r, g);
           if (kk >= Lk || (CAUSAL && kk > qrow)) p = 0.f;

@@ -31,17 +31,15 @@ constexpr float kLn2 = 0.6931471805599453f;
 
 __device__ __forceinline__ float bf16_to_f32(u16 b) { return __uint_as_float(uint32_t(b) << 16); }
 
-// Round-to-nearest-even float -> bf16 bits (NaN kept quiet).
-__device__ __forceinline__ u16 f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return u16((u >> 16) | 0x40);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u16(u >> 16);
-}
+// Round-to-nearest-even float -> bf16 bits (v_cvt_pk_bf16_f32 on gfx950;
+// NaN stays NaN).
+__device__ __forceinline__ u16 f32_to_bf16(float f) { return __builtin_bit_cast(u16, (__bf16)f); }
 
 // Two floats -> packed bf16x2 (low half = a), RNE.
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
-  return uint32_t(f32_to_bf16(a)) | (uint32_t(f32_to_bf16(b)) << 16);
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  bf16x2 v = {(__bf16)a, (__bf16)b};
+  return __builtin_bit_cast(uint32_t, v);
 }
 
 __device__ __forceinline__ f32x16 mfma_bf16_32x32x16(const bf16x8& a, const bf16x8& b, const f32x16& c) {
@@ -68,5 +66,53 @@ __device__ __forceinline__ float wave_xor32(float x) { return __shfl_xor(x, 32, 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 __device__ __forceinline__ uint4 ldg16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// ds_read_b64_tr_b16 (gfx950).  Within each 16-lane group, lane t receives
+// element t%4 of the 8-byte chunks addressed by lanes 4e + t/4, e = 0..3.
+// So if lane s of the group points at row (r0 + s/4), column (c0 + 4*(s%4))
+// of a row-major b16 matrix, lane t gets rows r0..r0+3 of column c0 + t:
+// four consecutive k-values of one column, the MFMA operand layout.
+__device__ __forceinline__ s16x4 lds_read_tr16(const u16* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p));
+}
+
+// Two transpose reads (rows r0..r0+3 and r1..r1+3 of one column) as one
+// bf16x8 MFMA operand.
+__device__ __forceinline__ bf16x8 lds_read_tr16x2(const u16* p0, const u16* p1) {
+  s16x4 a = lds_read_tr16(p0), b = lds_read_tr16(p1);
+  typedef short s16x8 __attribute__((ext_vector_type(8)));
+  s16x8 v = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+  return __builtin_bit_cast(bf16x8, v);
+}
+
+__device__ __forceinline__ bool wave_any(bool p) { return __any(p); }
+
+// Row-major bf16 tile of D columns in LDS, addressed by 16-byte chunks, that
+// serves two read patterns without bank conflicts:
+//   * 16-byte row reads: 16 lanes read one chunk of 16 consecutive rows;
+//   * transpose reads: 32 lanes read 4 consecutive 8-byte pieces of each of
+//     4 consecutive rows (rows r0..r0+3 with r0 % 4 == 0).
+// For D = 128 (256-byte rows, no padding) chunk c of row r is stored at
+// chunk c ^ h(r), h(r) = ((r & 3) << 2) | ((r >> 2) & 3): 16 consecutive rows
+// map one chunk to 16 distinct bank groups, and 4 aligned rows x 4 aligned
+// chunks map to 16 distinct bank groups.  Narrower tiles pad rows by 16
+// bytes instead.
+template <int D>
+struct SwzTile {
+  static constexpr int kPitch = D == 128 ? 128 : D + 8;
+  static constexpr int kElems(int rows) { return rows * kPitch; }
+  // element offset of chunk `ch` (8 elements) of row `row`
+  __device__ static __forceinline__ int chunk(int row, int ch) {
+    if constexpr (D == 128)
+      return row * 128 + 8 * (ch ^ (((row & 3) << 2) | ((row >> 2) & 3)));
+    else
+      return row * kPitch + 8 * ch;
+  }
+  // element offset of column `col` (a multiple of 4) of row `row`
+  __device__ static __forceinline__ int at4(int row, int col) { return chunk(row, col >> 3) + (col & 4); }
+};
 
 }  // namespace tt

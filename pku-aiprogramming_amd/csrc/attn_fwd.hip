@@ -17,6 +17,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cmath>
+#include <type_traits>
 
 #include "attn_common.h"
 #include "attn_tiles.h"
@@ -32,14 +33,14 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(
     u16* __restrict__ O, float* __restrict__ LSE, int Lq, int Lk, int BH, int nqt, int group,
     float sl2) {
   constexpr int BM = FWD_BM, BN = FWD_BN;
-  constexpr int KP = D + 8;   // sK row pitch (elements): 16-byte aligned, rows shift 4 banks
-  constexpr int VP = BN + 8;  // sVt row pitch
-  constexpr int NC = D / 16;  // 16-wide k-chunks of the d contraction
-  constexpr int ND = D / 32;  // 32-row tiles of O^T
-  constexpr int CPR = D / 8;  // 16-byte chunks per row
-  constexpr int LPT = BN * CPR / 256;  // chunks per thread per tile
+  constexpr int KP = D + 8;                   // sK pitch: 16-byte row reads, rows shift 4 banks
+  constexpr int VP = D == 32 ? 32 : D + 32;   // sV pitch: 4 rows of a transpose read hit 4 bank quarters
+  constexpr int NC = D / 16;                  // 16-wide k-chunks of the d contraction
+  constexpr int ND = D / 32;                  // 32-row tiles of O^T
+  constexpr int CPR = D / 8;                  // 16-byte chunks per row
+  constexpr int LPT = BN * CPR / 256;         // chunks per thread per tile
   __shared__ __align__(16) u16 sK[BN * KP];
-  __shared__ __align__(16) u16 sVt[D * VP];
+  __shared__ __align__(16) u16 sV[BN * VP];
 
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, g = l >> 5, r32 = l & 31;
   int qt, bh;
@@ -50,35 +51,37 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(
   const int64_t kbase = (int64_t)bh * Lk * D;
 
   bf16x8 qf[NC];
+  {
+    const int qr = min(qrow, Lq - 1);  // padding rows read a valid row; never written back
 #pragma unroll
-  for (int c = 0; c < NC; ++c) {
-    if (qrow < Lq) {
-      uint4 t = ldg16(Q + qbase + (int64_t)qrow * D + 16 * c + 8 * g);
-      qf[c] = *reinterpret_cast<bf16x8*>(&t);
-    } else {
-      uint4 z = {0, 0, 0, 0};
-      qf[c] = *reinterpret_cast<bf16x8*>(&z);
+    for (int c = 0; c < NC; ++c) {
+      uint4 t = ldg16(Q + qbase + (int64_t)qr * D + 16 * c + 8 * g);
+      qf[c] = __builtin_bit_cast(bf16x8, t);
     }
   }
 
   f32x16 acc[ND];
 #pragma unroll
   for (int dt = 0; dt < ND; ++dt) acc[dt] = f32x16{};
-  float m = -INFINITY, lsum = 0.f;
+  float m = -INFINITY;  // running max of the scaled scores, log2 domain (may lag, see below)
+  float lsum = 0.f;     // this lane's share of the running sum
 
   const int kend = CAUSAL ? min(Lk, q0 + BM) : Lk;
   const int wq_lo = q0 + 32 * w, wq_hi = wq_lo + 31;
+
+  // Transpose-read addressing of the V^T operand (lane = source row/col).
+  const int t16 = l & 15;
+  const int vcol = 16 * ((l >> 4) & 1) + 4 * (t16 & 3);
+  const int vrow = 4 * g + (t16 >> 2);
 
   uint4 kreg[LPT], vreg[LPT];
   auto gload = [&](int kb) {
 #pragma unroll
     for (int i = 0; i < LPT; ++i) {
       const int c = tid + 256 * i;
-      const int key = c / CPR, ch = c % CPR;  // K: row-major order, coalesced
-      const int vkey = c % BN, vch = c / BN;  // V: key-fastest, conflict-free transpose
-      uint4 z = {0, 0, 0, 0};
-      kreg[i] = (kb + key < Lk) ? ldg16(K + kbase + (int64_t)(kb + key) * D + 8 * ch) : z;
-      vreg[i] = (kb + vkey < Lk) ? ldg16(V + kbase + (int64_t)(kb + vkey) * D + 8 * vch) : z;
+      const int key = min(kb + c / CPR, Lk - 1), ch = c % CPR;  // rows past Lk are masked
+      kreg[i] = ldg16(K + kbase + (int64_t)key * D + 8 * ch);
+      vreg[i] = ldg16(V + kbase + (int64_t)key * D + 8 * ch);
     }
   };
   auto sstore = [&]() {
@@ -87,12 +90,73 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(
       const int c = tid + 256 * i;
       const int key = c / CPR, ch = c % CPR;
       *reinterpret_cast<uint4*>(&sK[key * KP + 8 * ch]) = kreg[i];
-      const int vkey = c % BN, vch = c / BN;
-      const u16* e = reinterpret_cast<const u16*>(&vreg[i]);
-      const int pos = perm16(vkey);
-#pragma unroll
-      for (int x = 0; x < 8; ++x) sVt[(8 * vch + x) * VP + pos] = e[x];
+      *reinterpret_cast<uint4*>(&sV[key * VP + 8 * ch]) = vreg[i];
     }
+  };
+
+  auto tile = [&](int kb, auto mask_tag) {
+    constexpr bool MASK = decltype(mask_tag)::value;
+    f32x16 s[2] = {f32x16{}, f32x16{}};
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        bf16x8 a = *reinterpret_cast<const bf16x8*>(&sK[(32 * t + r32) * KP + 16 * c + 8 * g]);
+        s[t] = mfma_bf16_32x32x16(a, qf[c], s[t]);
+      }
+    if constexpr (MASK) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = kb + 32 * t + acc_row(r, g);
+          if (key >= Lk || (CAUSAL && key > qrow)) s[t][r] = -INFINITY;
+        }
+    }
+    float mx = s[0][0];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[t][r]);
+    mx = fmaxf(mx, wave_xor32(mx)) * sl2;
+    // Lazy rescale: the running max only moves when some lane's tile max
+    // exceeds it by more than 8 (log2 units), so p = 2^(x - m) <= 256 and the
+    // O / sum rescale is skipped on most tiles.  The result is exact either
+    // way: numerator and denominator share the same m.
+    if (wave_any(mx > m + 8.f)) {
+      const float mnew = fmaxf(m, mx);
+      const float alpha = fast_exp2(m - mnew);  // 0 when m = -inf
+      lsum *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < ND; ++dt) acc[dt] *= alpha;
+      m = mnew;
+    }
+    const float mb = (m == -INFINITY) ? 0.f : m;
+    float ps = 0.f;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = fast_exp2(fmaf(s[t][r], sl2, -mb));
+        s[t][r] = p;
+        ps += p;
+      }
+    lsum += ps;
+    bf16x8 pb[4];
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) pb[kc][e] = (__bf16)s[kc >> 1][8 * (kc & 1) + e];
+    // O^T += V^T P^T; chunk kc holds keys 16kc + perm16 order, read by two
+    // transpose reads of 4 consecutive keys each.
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc)
+#pragma unroll
+      for (int dt = 0; dt < ND; ++dt) {
+        const u16* p0 = &sV[(16 * kc + vrow) * VP + 32 * dt + vcol];
+        bf16x8 a = lds_read_tr16x2(p0, p0 + 8 * VP);
+        acc[dt] = mfma_bf16_32x32x16(a, pb[kc], acc[dt]);
+      }
   };
 
   if (kend > 0) gload(0);
@@ -102,63 +166,10 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(
     __syncthreads();
     if (kb + BN < kend) gload(kb + BN);
     if (CAUSAL && kb > wq_hi) continue;  // every key of the tile is after every query of the wave
-
-    f32x16 s[2];
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      s[t] = f32x16{};
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        bf16x8 a = *reinterpret_cast<const bf16x8*>(&sK[(32 * t + r32) * KP + 16 * c + 8 * g]);
-        s[t] = mfma_bf16_32x32x16(a, qf[c], s[t]);
-      }
-    }
-
-    const bool need_mask = (kb + BN > Lk) || (CAUSAL && kb + BN - 1 > wq_lo);
-    float mx = -INFINITY;
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float x = s[t][r] * sl2;
-        if (need_mask) {
-          const int key = kb + 32 * t + acc_row(r, g);
-          if (key >= Lk || (CAUSAL && key > qrow)) x = -INFINITY;
-        }
-        s[t][r] = x;
-        mx = fmaxf(mx, x);
-      }
-    mx = fmaxf(mx, wave_xor32(mx));
-    const float mnew = fmaxf(m, mx);
-    const float mb = (mnew == -INFINITY) ? 0.f : mnew;
-    const float alpha = fast_exp2(m - mb);
-    m = mnew;
-    float ps = 0.f;
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float p = fast_exp2(s[t][r] - mb);
-        s[t][r] = p;
-        ps += p;
-      }
-    lsum = lsum * alpha + ps;
-#pragma unroll
-    for (int dt = 0; dt < ND; ++dt) acc[dt] *= alpha;
-
-    bf16x8 pb[4];
-#pragma unroll
-    for (int kc = 0; kc < 4; ++kc)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) pb[kc][e] = (__bf16)s[kc >> 1][8 * (kc & 1) + e];
-
-#pragma unroll
-    for (int dt = 0; dt < ND; ++dt)
-#pragma unroll
-      for (int kc = 0; kc < 4; ++kc) {
-        bf16x8 a = *reinterpret_cast<const bf16x8*>(&sVt[(32 * dt + r32) * VP + 16 * kc + 8 * g]);
-        acc[dt] = mfma_bf16_32x32x16(a, pb[kc], acc[dt]);
-      }
+    if ((kb + BN > Lk) || (CAUSAL && kb + BN - 1 > wq_lo))
+      tile(kb, std::true_type{});
+    else
+      tile(kb, std::false_type{});
   }
 
   lsum += wave_xor32(lsum);
