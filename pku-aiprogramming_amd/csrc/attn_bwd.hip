@@ -622,11 +622,11 @@ static int bwd_entry(const char* fn, const T* q, const T* k, const T* v, const T
   if (rc) return rc;
   const int64_t BH = B * H;
   if (BH == 0) return ok();
-  if ((rc = ensure_init())) return rc;
-  hipStream_t st = stream_or_default(stream);
   if (Lq == 0) {  // no queries: every key gets zero gradient
     if (Lk > 0) {
       if (!dk || !dv) return fail(TT_ERR_ARG, std::string(fn) + ": null pointer");
+      if ((rc = ensure_init())) return rc;
+      hipStream_t st = stream_or_default(stream);
       TT_HIP(hipMemsetAsync(dk, 0, (size_t)(BH * Lk * d) * sizeof(T), st));
       TT_HIP(hipMemsetAsync(dv, 0, (size_t)(BH * Lk * d) * sizeof(T), st));
     }
@@ -634,6 +634,8 @@ static int bwd_entry(const char* fn, const T* q, const T* k, const T* v, const T
   }
   if (!q || !k || !v || !o || !lse || !dout || !dq || !dk || !dv)
     return fail(TT_ERR_ARG, std::string(fn) + ": null pointer");
+  if ((rc = ensure_init())) return rc;
+  hipStream_t st = stream_or_default(stream);
   switch (d * 2 + (causal ? 1 : 0)) {
     case 64: return launch_bwd<T, 32, false>(q, k, v, o, lse, dout, dq, dk, dv, BH, Lq, Lk, scale, st);
     case 65: return launch_bwd<T, 32, true>(q, k, v, o, lse, dout, dq, dk, dv, BH, Lq, Lk, scale, st);
