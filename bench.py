@@ -43,6 +43,24 @@ C5 = dict(B=4, H=32, L=4096, d=128)
 C4 = dict(B=64, H=32, Lkv=8192, d=128)
 
 
+# HBM bytes per launch measured by two rocprofv3 PMC runs (FETCH_SIZE, then
+# WRITE_SIZE), scaled by a 1 GiB copy kernel's readings (fetch x2.000,
+# write x1.000); the commands and raw counters are in
+# profiles/hbm_traffic_c5_c4.md.  Re-measured whenever a kernel changes.
+MEASURED_TRAFFIC_MIB = {
+    "attn_fwd": 648.8,
+    "attn_bwd_delta": 258.0,
+    "attn_bwd_dkdv": 772.3,
+    "attn_bwd_dq": 644.2,
+    "attn_decode_split": 8217.6,
+}
+
+
+def traffic_bytes(kernel):
+    mib = MEASURED_TRAFFIC_MIB.get(kernel)
+    return None if mib is None else mib * 2 ** 20
+
+
 def fwdbwd_flops(B, H, L, d, causal=True):
     f = 12.0 * B * H * L * L * d
     return f / 2 if causal else f
@@ -129,6 +147,31 @@ def run_decode(T, steps, warmup):
     return total_ms / steps, per
 
 
+def run_copy(T, steps, warmup, nbytes=1 << 30):
+    """Plain fp32 copy (c = 1.0 * a) of `nbytes`: reads and writes exactly
+    nbytes each, used to calibrate the profiler's FETCH_SIZE / WRITE_SIZE."""
+    n = nbytes // 4
+    a = T.DeviceBuffer((n,), "f32")
+    c = T.DeviceBuffer((n,), "f32")
+    a.fill_normal(1)
+    L = T.lib()
+
+    def once():
+        L.call("tt_elementwise", 4, 0, c.ptr, a.ptr, None, n, 1.0, 0.0, 0, None)  # TT_EW_SCALE, TT_F32
+
+    for _ in range(warmup):
+        once()
+    start, stop = T.Event(), T.Event()
+    L.sync()
+    start.record()
+    for _ in range(steps):
+        once()
+    stop.record()
+    L.sync()
+    ms = T.Event.elapsed(start, stop) / steps
+    return ms, 2 * nbytes / (ms * 1e-3) / 1e9
+
+
 def cpu_baseline(sample_heads):
     """The reference's op chain in float32 numpy on `sample_heads` heads of
     the headline workload (1 warm-up head, not counted)."""
@@ -174,8 +217,8 @@ def main(argv=None):
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", choices=["all", "fwdbwd", "decode"], default="all",
-                    help="run one workload only (for profiler runs)")
+    ap.add_argument("--only", choices=["all", "fwdbwd", "decode", "copy"], default="all",
+                    help="run one workload only (for profiler runs; 'copy' is the 1 GiB calibration copy)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-heads", type=int, default=128)
     args = ap.parse_args(argv)
@@ -202,6 +245,12 @@ def main(argv=None):
                    "flop_per_step": fwdbwd_flops(**C5)},
     }
 
+    if args.only == "copy":
+        ms, gbs = run_copy(T, args.steps, args.warmup)
+        print(json.dumps({"metric": "calibration copy GB/s (1 GiB read + 1 GiB write)", "value": gbs,
+                          "unit": "GB/s", "ms_per_step": ms, "steps": args.steps}), flush=True)
+        return 0
+
     if args.only in ("all", "fwdbwd"):
         ms, per = run_fwdbwd(T, args.steps, args.warmup)
         flops = fwdbwd_flops(**C5)
@@ -217,7 +266,7 @@ def main(argv=None):
         dom = max(per, key=per.get)
         ach = kf[dom] / (per[dom] * 1e-3) / 1e12
         out["roofline"] = {"bound": "mfma", "kernel": dom, "achieved": ach, "peak": PEAK_BF16_TFLOPS,
-                           "unit": "TFLOP/s", "frac": ach / PEAK_BF16_TFLOPS, "traffic": None,
+                           "unit": "TFLOP/s", "frac": ach / PEAK_BF16_TFLOPS, "traffic": traffic_bytes(dom),
                            "algorithmic_flop_per_launch": kf[dom]}
 
     if args.only in ("all", "decode"):
@@ -232,7 +281,7 @@ def main(argv=None):
             "ms_per_step": ms, "frac_of_peak": gbs / PEAK_HBM_GBS, "bytes_per_step": nbytes,
             "kernels": {n: {"avg_ms": t} for n, t in per.items()},
             "roofline": {"bound": "hbm", "kernel": "attn_decode_split", "achieved": sgbs, "peak": PEAK_HBM_GBS,
-                         "unit": "GB/s", "frac": sgbs / PEAK_HBM_GBS, "traffic": None,
+                         "unit": "GB/s", "frac": sgbs / PEAK_HBM_GBS, "traffic": traffic_bytes("attn_decode_split"),
                          "algorithmic_bytes_per_launch": split_bytes},
         }
         if args.only == "decode":

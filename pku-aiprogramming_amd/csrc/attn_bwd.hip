@@ -34,15 +34,19 @@
 namespace tt {
 
 constexpr int DKDV_BN = 128;  // keys per workgroup
-constexpr int DKDV_BQ = 64;   // queries per LDS step
+constexpr int DKDV_BQ = 64;   // queries per LDS step (fp32 kernel)
 constexpr int DQ_BM = 128;    // queries per workgroup
 constexpr int DQ_BN = 64;     // keys per LDS step
 
-// D_i = sum_d dO[i][d] * O[i][d], one 16-byte chunk per thread.
+// D_i = sum_d dO[i][d] * O[i][d], one 16-byte chunk per thread; also
+// L2_i = LSE_i * log2(e), the log-sum-exp in the log2 domain the MFMA
+// kernels exponentiate in.
 template <typename T, int D>
 __global__ __launch_bounds__(256) void attn_bwd_delta_kernel(const T* __restrict__ O,
                                                              const T* __restrict__ dO,
-                                                             float* __restrict__ Delta, int64_t rows) {
+                                                             const float* __restrict__ LSE,
+                                                             float* __restrict__ Delta, float* __restrict__ L2,
+                                                             int64_t rows) {
   constexpr int EPT = 16 / sizeof(T);
   constexpr int TPR = D / EPT;  // threads per row (a power of two <= 32)
   constexpr int RPB = 256 / TPR;
@@ -66,24 +70,36 @@ __global__ __launch_bounds__(256) void attn_bwd_delta_kernel(const T* __restrict
   }
 #pragma unroll
   for (int off = TPR / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
-  if (col == 0 && row < rows) Delta[row] = sum;
+  if (col == 0 && row < rows) {
+    Delta[row] = sum;
+    L2[row] = LSE[row] * kLog2e;
+  }
 }
 
 // ------------------------------------------------------------------ bf16 dK, dV
+// Query rows per LDS step of the dK/dV kernel: 32 at d = 128 keeps the
+// double-buffered Q / dO tiles plus the V tile at 64.5 KB, so two
+// workgroups (2 waves per SIMD) share a CU.
+constexpr int dkdv_bq(int D) { return D == 128 ? 32 : 64; }
+
 template <int D, bool CAUSAL>
-__global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_bf16_kernel(
+__global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_bf16_kernel(
     const u16* __restrict__ Q, const u16* __restrict__ K, const u16* __restrict__ V,
-    const u16* __restrict__ dO, const float* __restrict__ LSE, const float* __restrict__ Delta,
+    const u16* __restrict__ dO, const float* __restrict__ L2, const float* __restrict__ Delta,
     u16* __restrict__ dK, u16* __restrict__ dV, int Lq, int Lk, int BH, int nkt, int group, float sl2,
     float scale) {
   using Tile = SwzTile<D>;
-  constexpr int BN = DKDV_BN, BQ = DKDV_BQ;
-  constexpr int NC = D / 16, ND = D / 32, CPR = D / 8;
-  constexpr int LPT = BQ * CPR / 256;
-  __shared__ __align__(16) u16 sQ[Tile::kElems(BQ)];
-  __shared__ __align__(16) u16 sdO[Tile::kElems(BQ)];
-  __shared__ __align__(16) float sL[BQ];
-  __shared__ __align__(16) float sDl[BQ];
+  constexpr int BN = DKDV_BN, BQ = dkdv_bq(D), MT = BQ / 32;
+  constexpr int NC = D / 16, ND = D / 32;
+  constexpr int TE = Tile::kElems(BQ);
+  constexpr int VS = 64;  // stride of the LSE / D row buffers (one 64-lane load each)
+  // Q / dO tiles and their LSE (log2) / D rows, double-buffered, and the
+  // workgroup's V rows, all filled by direct global->LDS loads
+  __shared__ __align__(16) u16 sQ[2 * TE];
+  __shared__ __align__(16) u16 sdO[2 * TE];
+  __shared__ __align__(16) u16 sV[Tile::kElems(BN)];
+  __shared__ __align__(16) float sL[2 * VS];
+  __shared__ __align__(16) float sDl[2 * VS];
 
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, g = l >> 5, r32 = l & 31;
   int kt, bh;
@@ -95,15 +111,14 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_bf16_kernel(
   const int64_t kbase = (int64_t)bh * Lk * D;
   const int64_t lbase = (int64_t)bh * Lq;
 
-  bf16x8 kf[NC], vf[NC];
+  bf16x8 kf[NC];
   {
     const int kr = min(key, Lk - 1);  // rows past Lk compute garbage that is never stored
 #pragma unroll
-    for (int c = 0; c < NC; ++c) {
+    for (int c = 0; c < NC; ++c)
       kf[c] = __builtin_bit_cast(bf16x8, ldg16(K + kbase + (int64_t)kr * D + 16 * c + 8 * g));
-      vf[c] = __builtin_bit_cast(bf16x8, ldg16(V + kbase + (int64_t)kr * D + 16 * c + 8 * g));
-    }
   }
+  load_tile_lds<D, BN>(V + kbase, k0, Lk, sV);  // published by the first loop barrier
   f32x16 adk[ND], adv[ND];
 #pragma unroll
   for (int dt = 0; dt < ND; ++dt) adk[dt] = adv[dt] = f32x16{};
@@ -113,62 +128,45 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_bf16_kernel(
   const int trow = 4 * g + (t16 >> 2);
   const int tcol = 16 * ((l >> 4) & 1) + 4 * (t16 & 3);
 
-  uint4 qreg[LPT], oreg[LPT];
-  float lreg = 0.f, dreg = 0.f;
-  auto gload = [&](int qb) {
-#pragma unroll
-    for (int i = 0; i < LPT; ++i) {
-      const int c = tid + 256 * i;
-      const int row = min(qb + c / CPR, Lq - 1), ch = c % CPR;
-      qreg[i] = ldg16(Q + qbase + (int64_t)row * D + 8 * ch);
-      oreg[i] = ldg16(dO + qbase + (int64_t)row * D + 8 * ch);
-    }
-    if (tid < BQ) {
-      const bool in = qb + tid < Lq;
-      lreg = in ? LSE[lbase + qb + tid] * kLog2e : INFINITY;  // +inf -> P = 0 for padding rows
-      dreg = in ? Delta[lbase + qb + tid] : 0.f;
-    }
-  };
-  auto sstore = [&]() {
-#pragma unroll
-    for (int i = 0; i < LPT; ++i) {
-      const int c = tid + 256 * i;
-      const int row = c / CPR, ch = c % CPR;
-      *reinterpret_cast<uint4*>(&sQ[Tile::chunk(row, ch)]) = qreg[i];
-      *reinterpret_cast<uint4*>(&sdO[Tile::chunk(row, ch)]) = oreg[i];
-    }
-    if (tid < BQ) {
-      sL[tid] = lreg;
-      sDl[tid] = dreg;
+  // Query rows past Lq read row Lq - 1 and are masked (P = 0) in the edge step.
+  auto issue = [&](int qb, int buf) {
+    load_tile_lds<D, BQ>(Q + qbase, qb, Lq, sQ + buf * TE);
+    load_tile_lds<D, BQ>(dO + qbase, qb, Lq, sdO + buf * TE);
+    if (w == 0) {
+      load_vec_lds(L2 + lbase + qb, Lq - qb, sL + buf * VS);
+      load_vec_lds(Delta + lbase + qb, Lq - qb, sDl + buf * VS);
     }
   };
 
-  auto step = [&](int qb, auto mask_tag) {
+  auto step = [&](int qb, const u16* tQ, const u16* tdO, const float* tL, const float* tD, auto mask_tag) {
     constexpr bool MASK = decltype(mask_tag)::value;
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
+    for (int mt = 0; mt < MT; ++mt) {
       f32x16 s = f32x16{}, dp = f32x16{};
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
         const int off = Tile::chunk(32 * mt + r32, 2 * c + g);
-        s = mfma_bf16_32x32x16(*reinterpret_cast<const bf16x8*>(&sQ[off]), kf[c], s);
-        dp = mfma_bf16_32x32x16(*reinterpret_cast<const bf16x8*>(&sdO[off]), vf[c], dp);
+        s = mfma_bf16_32x32x16(*reinterpret_cast<const bf16x8*>(&tQ[off]), kf[c], s);
+        const bf16x8 vb = *reinterpret_cast<const bf16x8*>(&sV[Tile::chunk(32 * w + r32, 2 * c + g)]);
+        dp = mfma_bf16_32x32x16(*reinterpret_cast<const bf16x8*>(&tdO[off]), vb, dp);
       }
       // s[r] = S[query qb + 32mt + acc_row(r, g)][key]
       bf16x8 pb[2], db[2];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int qi = 32 * mt + 8 * j + 4 * g;  // rows acc_row(4j..4j+3, g)
-        const float4 lv = *reinterpret_cast<const float4*>(&sL[qi]);
-        const float4 dv = *reinterpret_cast<const float4*>(&sDl[qi]);
+        const float4 lv = *reinterpret_cast<const float4*>(&tL[qi]);
+        const float4 dv = *reinterpret_cast<const float4*>(&tD[qi]);
         const float la[4] = {lv.x, lv.y, lv.z, lv.w};
         const float da[4] = {dv.x, dv.y, dv.z, dv.w};
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
           const int r = 4 * j + u;
           float p = fast_exp2(fmaf(s[r], sl2, -la[u]));
-          if constexpr (MASK)
-            if (key > qb + qi + u) p = 0.f;
+          if constexpr (MASK) {
+            const int q = qb + qi + u;
+            if (q >= Lq || (CAUSAL && key > q)) p = 0.f;
+          }
           pb[r >> 3][r & 7] = (__bf16)p;
           db[r >> 3][r & 7] = (__bf16)(p * (dp[r] - da[u]));
         }
@@ -181,25 +179,32 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_bf16_kernel(
         for (int dt = 0; dt < ND; ++dt) {
           const int r0 = 32 * mt + 16 * h + trow;
           const int o0 = Tile::at4(r0, 32 * dt + tcol), o1 = Tile::at4(r0 + 8, 32 * dt + tcol);
-          adv[dt] = mfma_bf16_32x32x16(lds_read_tr16x2(&sdO[o0], &sdO[o1]), pb[h], adv[dt]);
-          adk[dt] = mfma_bf16_32x32x16(lds_read_tr16x2(&sQ[o0], &sQ[o1]), db[h], adk[dt]);
+          adv[dt] = mfma_bf16_32x32x16(lds_read_tr16x2(&tdO[o0], &tdO[o1]), pb[h], adv[dt]);
+          adk[dt] = mfma_bf16_32x32x16(lds_read_tr16x2(&tQ[o0], &tQ[o1]), db[h], adk[dt]);
         }
     }
   };
 
-  const int qstart = CAUSAL ? (k0 / BQ) * BQ : 0;
-  if (qstart < Lq) gload(qstart);
-  for (int qb = qstart; qb < Lq; qb += BQ) {
-    __syncthreads();
-    sstore();
-    __syncthreads();
-    if (qb + BQ < Lq) gload(qb + BQ);
-    if (CAUSAL && qb + BQ - 1 < wk_lo) continue;  // every query of the tile precedes every key of the wave
-    if (CAUSAL && qb < wk_lo + 31)
-      step(qb, std::true_type{});
-    else
-      step(qb, std::false_type{});
-  }
+  // Masked (diagonal / ragged) and unmasked query tiles run in separate
+  // loops so that neither loop switches the accumulators' registers.
+  int j = 0;
+  auto run = [&](int lo, int hi, auto mask_tag) {
+    for (int qb = lo; qb < hi; qb += BQ, ++j) {
+      wait_vmem();
+      __syncthreads();  // publishes tile j, retires all reads of the buffer refilled next
+      if (qb + BQ < Lq) issue(qb + BQ, (j + 1) & 1);
+      if (CAUSAL && qb + BQ - 1 < wk_lo) continue;  // every query of the tile precedes every key of the wave
+      const int b = j & 1;
+      step(qb, sQ + b * TE, sdO + b * TE, sL + b * VS, sDl + b * VS, mask_tag);
+    }
+  };
+  const int qstart = CAUSAL ? k0 : 0;  // k0 is a multiple of BQ
+  if (qstart < Lq) issue(qstart, 0);
+  const int qfull = (Lq / BQ) * BQ;
+  const int qdiag = CAUSAL ? min(k0 + BN, Lq) : qstart;  // [qstart, qdiag): tiles crossing the diagonal
+  run(qstart, qdiag, std::true_type{});
+  run(qdiag, qfull, std::false_type{});
+  run(max(qdiag, qfull), Lq, std::true_type{});
 
   if (key < Lk) {
     u16* dkrow = dK + kbase + (int64_t)key * D;
@@ -222,17 +227,17 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_bf16_kernel(
 
 // ------------------------------------------------------------------ bf16 dQ
 template <int D, bool CAUSAL>
-__global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void attn_bwd_dq_bf16_kernel(
+__global__ __launch_bounds__(256, 2) void attn_bwd_dq_bf16_kernel(
     const u16* __restrict__ Q, const u16* __restrict__ K, const u16* __restrict__ V,
-    const u16* __restrict__ dO, const float* __restrict__ LSE, const float* __restrict__ Delta,
+    const u16* __restrict__ dO, const float* __restrict__ L2, const float* __restrict__ Delta,
     u16* __restrict__ dQ, int Lq, int Lk, int BH, int nqt, int group, float sl2, float scale) {
   using Tile = SwzTile<D>;
   constexpr int BM = DQ_BM, BN = DQ_BN;
-  constexpr int VP = D + 8;
-  constexpr int NC = D / 16, ND = D / 32, CPR = D / 8;
-  constexpr int LPT = BN * CPR / 256;
-  __shared__ __align__(16) u16 sK[Tile::kElems(BN)];
-  __shared__ __align__(16) u16 sV[BN * VP];
+  constexpr int NC = D / 16, ND = D / 32;
+  constexpr int TE = Tile::kElems(BN);
+  // K / V tiles, double-buffered, filled by direct global->LDS loads
+  __shared__ __align__(16) u16 sK[2 * TE];
+  __shared__ __align__(16) u16 sV[2 * TE];
 
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, g = l >> 5, r32 = l & 31;
   int qt, bh;
@@ -252,7 +257,8 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void attn_bwd_dq_bf16_kern
       dof[c] = __builtin_bit_cast(bf16x8, ldg16(dO + qbase + (int64_t)qr * D + 16 * c + 8 * g));
     }
   }
-  const float lse2 = qrow < Lq ? LSE[(int64_t)bh * Lq + qrow] * kLog2e : INFINITY;
+  // padding query rows (qrow >= Lq): P = 2^(s - inf) = 0
+  const float lse2 = qrow < Lq ? L2[(int64_t)bh * Lq + qrow] : INFINITY;
   const float dl = qrow < Lq ? Delta[(int64_t)bh * Lq + qrow] : 0.f;
   f32x16 adq[ND];
 #pragma unroll
@@ -262,37 +268,22 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void attn_bwd_dq_bf16_kern
   const int trow = 4 * g + (t16 >> 2);
   const int tcol = 16 * ((l >> 4) & 1) + 4 * (t16 & 3);
 
-  uint4 kreg[LPT], vreg[LPT];
-  auto gload = [&](int kb) {
-#pragma unroll
-    for (int i = 0; i < LPT; ++i) {
-      const int c = tid + 256 * i;
-      const int row = min(kb + c / CPR, Lk - 1), ch = c % CPR;
-      kreg[i] = ldg16(K + kbase + (int64_t)row * D + 8 * ch);
-      vreg[i] = ldg16(V + kbase + (int64_t)row * D + 8 * ch);
-    }
-  };
-  auto sstore = [&]() {
-#pragma unroll
-    for (int i = 0; i < LPT; ++i) {
-      const int c = tid + 256 * i;
-      const int row = c / CPR, ch = c % CPR;
-      *reinterpret_cast<uint4*>(&sK[Tile::chunk(row, ch)]) = kreg[i];
-      *reinterpret_cast<uint4*>(&sV[row * VP + 8 * ch]) = vreg[i];
-    }
+  // key rows past Lk read row Lk - 1 and are masked (P = 0) in the edge tile
+  auto issue = [&](int kb, int buf) {
+    load_tile_lds<D, BN>(K + kbase, kb, Lk, sK + buf * TE);
+    load_tile_lds<D, BN>(V + kbase, kb, Lk, sV + buf * TE);
   };
 
-  auto tile = [&](int kb, auto mask_tag) {
+  auto tile = [&](int kb, const u16* tK, const u16* tV, auto mask_tag) {
     constexpr bool MASK = decltype(mask_tag)::value;
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       f32x16 s = f32x16{}, dp = f32x16{};
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
-        const bf16x8 a = *reinterpret_cast<const bf16x8*>(&sK[Tile::chunk(32 * t + r32, 2 * c + g)]);
-        s = mfma_bf16_32x32x16(a, qf[c], s);
-        const bf16x8 b = *reinterpret_cast<const bf16x8*>(&sV[(32 * t + r32) * VP + 16 * c + 8 * g]);
-        dp = mfma_bf16_32x32x16(b, dof[c], dp);
+        const int off = Tile::chunk(32 * t + r32, 2 * c + g);
+        s = mfma_bf16_32x32x16(*reinterpret_cast<const bf16x8*>(&tK[off]), qf[c], s);
+        dp = mfma_bf16_32x32x16(*reinterpret_cast<const bf16x8*>(&tV[off]), dof[c], dp);
       }
       bf16x8 db[2];
 #pragma unroll
@@ -309,25 +300,27 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void attn_bwd_dq_bf16_kern
 #pragma unroll
         for (int dt = 0; dt < ND; ++dt) {
           const int r0 = 32 * t + 16 * h + trow;
-          const bf16x8 a = lds_read_tr16x2(&sK[Tile::at4(r0, 32 * dt + tcol)], &sK[Tile::at4(r0 + 8, 32 * dt + tcol)]);
+          const bf16x8 a = lds_read_tr16x2(&tK[Tile::at4(r0, 32 * dt + tcol)], &tK[Tile::at4(r0 + 8, 32 * dt + tcol)]);
           adq[dt] = mfma_bf16_32x32x16(a, db[h], adq[dt]);
         }
     }
   };
 
   const int kend = CAUSAL ? min(Lk, q0 + BM) : Lk;
-  if (kend > 0) gload(0);
-  for (int kb = 0; kb < kend; kb += BN) {
-    __syncthreads();
-    sstore();
-    __syncthreads();
-    if (kb + BN < kend) gload(kb + BN);
-    if (CAUSAL && kb > wq_hi) continue;
-    if ((kb + BN > Lk) || (CAUSAL && kb + BN - 1 > wq_lo))
-      tile(kb, std::true_type{});
-    else
-      tile(kb, std::false_type{});
-  }
+  int j = 0;
+  auto run = [&](int lo, int hi, auto mask_tag) {
+    for (int kb = lo; kb < hi; kb += BN, ++j) {
+      wait_vmem();
+      __syncthreads();  // publishes tile j, retires all reads of the buffer refilled next
+      if (kb + BN < kend) issue(kb + BN, (j + 1) & 1);
+      if (CAUSAL && kb > wq_hi) continue;
+      tile(kb, sK + (j & 1) * TE, sV + (j & 1) * TE, mask_tag);
+    }
+  };
+  if (kend > 0) issue(0, 0);
+  const int kfull = CAUSAL ? min(q0, (Lk / BN) * BN) : (Lk / BN) * BN;  // unmasked tiles
+  run(0, kfull, std::false_type{});
+  run(kfull, kend, std::true_type{});
 
   if (qrow < Lq) {
     u16* row = dQ + qbase + (int64_t)qrow * D;
@@ -581,14 +574,17 @@ template <typename T, int D, bool CAUSAL>
 static int launch_bwd(const T* q, const T* k, const T* v, const T* o, const float* lse, const T* dout,
                       T* dq, T* dk, T* dv, int64_t BH, int64_t Lq, int64_t Lk, float scale, hipStream_t st) {
   constexpr bool BF = sizeof(T) == 2;
+  // workspace: D (row sums of dO o O) and LSE * log2(e), fp32 [B*H*Lq] each
   float* delta = nullptr;
-  int rc = workspace(0, (size_t)(BH * Lq) * sizeof(float), (void**)&delta);
+  int rc = workspace(0, (size_t)(2 * BH * Lq) * sizeof(float), (void**)&delta);
   if (rc) return rc;
   const int64_t rows = BH * Lq;
+  float* l2 = delta + rows;
   constexpr int TPR = D / (16 / (int)sizeof(T));
   const int64_t dblk = (rows + (256 / TPR) - 1) / (256 / TPR);
   if (dblk > 0x7fffffff) return fail(TT_ERR_ARG, "attention backward: grid too large");
-  hipLaunchKernelGGL((attn_bwd_delta_kernel<T, D>), dim3((unsigned)dblk), dim3(256), 0, st, o, dout, delta, rows);
+  hipLaunchKernelGGL((attn_bwd_delta_kernel<T, D>), dim3((unsigned)dblk), dim3(256), 0, st, o, dout, lse, delta,
+                     l2, rows);
   TT_LAUNCHED("attention backward delta launch", st);
 
   const float sl2 = scale * kLog2e;
@@ -598,10 +594,10 @@ static int launch_bwd(const T* q, const T* k, const T* v, const T* o, const floa
   const int gk = pick_group(BH, nkt, 32), gq = pick_group(BH, nqt, 32);
   if constexpr (BF) {
     hipLaunchKernelGGL((attn_bwd_dkdv_bf16_kernel<D, CAUSAL>), dim3((unsigned)(nkt * BH)), dim3(256), 0, st,
-                       q, k, v, dout, lse, delta, dk, dv, (int)Lq, (int)Lk, (int)BH, (int)nkt, gk, sl2, scale);
+                       q, k, v, dout, l2, delta, dk, dv, (int)Lq, (int)Lk, (int)BH, (int)nkt, gk, sl2, scale);
     TT_LAUNCHED("attention backward dK/dV launch", st);
     hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<D, CAUSAL>), dim3((unsigned)(nqt * BH)), dim3(256), 0, st,
-                       q, k, v, dout, lse, delta, dq, (int)Lq, (int)Lk, (int)BH, (int)nqt, gq, sl2, scale);
+                       q, k, v, dout, l2, delta, dq, (int)Lq, (int)Lk, (int)BH, (int)nqt, gq, sl2, scale);
     TT_LAUNCHED("attention backward dQ launch", st);
   } else {
     hipLaunchKernelGGL((attn_bwd_dkdv_f32_kernel<D, CAUSAL>), dim3((unsigned)(nkt * BH)), dim3(256), 0, st,

@@ -90,29 +90,69 @@ __device__ __forceinline__ bf16x8 lds_read_tr16x2(const u16* p0, const u16* p1) 
 
 __device__ __forceinline__ bool wave_any(bool p) { return __any(p); }
 
-// Row-major bf16 tile of D columns in LDS, addressed by 16-byte chunks, that
-// serves two read patterns without bank conflicts:
+// Dense row-major bf16 tile of D columns in LDS, addressed by 16-byte
+// chunks, that serves two read patterns without bank conflicts:
 //   * 16-byte row reads: 16 lanes read one chunk of 16 consecutive rows;
 //   * transpose reads: 32 lanes read 4 consecutive 8-byte pieces of each of
 //     4 consecutive rows (rows r0..r0+3 with r0 % 4 == 0).
-// For D = 128 (256-byte rows, no padding) chunk c of row r is stored at
-// chunk c ^ h(r), h(r) = ((r & 3) << 2) | ((r >> 2) & 3): 16 consecutive rows
-// map one chunk to 16 distinct bank groups, and 4 aligned rows x 4 aligned
-// chunks map to 16 distinct bank groups.  Narrower tiles pad rows by 16
-// bytes instead.
+// Chunk c of row r is stored at chunk c ^ sw(r) of that row.  With 256-byte
+// bank lines (64 banks x 4 bytes) the swizzle spreads both patterns over 16
+// distinct 16-byte bank groups:
+//   D = 128 (one row per line):    sw = ((r & 3) << 2) | ((r >> 2) & 3)
+//   D = 64  (two rows per line):   sw = (((r >> 1) & 1) << 2) | ((r >> 2) & 3)
+//   D = 32  (four rows per line):  sw = (r >> 2) & 3
+// The tile has no padding, so a wave's 64 consecutive 16-byte slots can be
+// filled by one direct global->LDS load (see load_tile_lds).
 template <int D>
 struct SwzTile {
-  static constexpr int kPitch = D == 128 ? 128 : D + 8;
-  static constexpr int kElems(int rows) { return rows * kPitch; }
-  // element offset of chunk `ch` (8 elements) of row `row`
-  __device__ static __forceinline__ int chunk(int row, int ch) {
-    if constexpr (D == 128)
-      return row * 128 + 8 * (ch ^ (((row & 3) << 2) | ((row >> 2) & 3)));
-    else
-      return row * kPitch + 8 * ch;
+  static constexpr int kCPR = D / 8;  // chunks per row
+  static constexpr int kElems(int rows) { return rows * D; }
+  __device__ static __forceinline__ constexpr int sw(int r) {
+    if constexpr (D == 128) return ((r & 3) << 2) | ((r >> 2) & 3);
+    if constexpr (D == 64) return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
+    return (r >> 2) & 3;
   }
+  // element offset of chunk `ch` (8 elements) of row `row`
+  __device__ static __forceinline__ int chunk(int row, int ch) { return row * D + 8 * (ch ^ sw(row)); }
   // element offset of column `col` (a multiple of 4) of row `row`
   __device__ static __forceinline__ int at4(int row, int col) { return chunk(row, col >> 3) + (col & 4); }
 };
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// Issue direct global->LDS loads (global_load_lds_dwordx4) of rows
+// [row0, row0 + ROWS) of a row-major [*, D] bf16 matrix into the SwzTile
+// `dst`.  Rows >= rmax read row rmax - 1 instead (callers mask them).  All
+// 256 threads take part; every wave instruction fills 64 consecutive 16-byte
+// LDS slots, each lane fetching the global chunk that belongs in its slot.
+// Completion: wait_vmem() then a barrier.
+template <int D, int ROWS>
+__device__ __forceinline__ void load_tile_lds(const u16* __restrict__ src, int row0, int rmax, u16* dst) {
+  constexpr int CPR = D / 8;
+  constexpr int ITERS = ROWS * CPR / 256;
+  static_assert(ROWS * CPR % 256 == 0, "tile must be a whole number of 256-chunk rounds");
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l = threadIdx.x & 63;
+#pragma unroll
+  for (int i = 0; i < ITERS; ++i) {
+    const int slot0 = (i * 4 + w) * 64;  // first slot of this wave instruction (wave-uniform)
+    const int p = slot0 + l;
+    const int row = p / CPR, phys = p % CPR;
+    const int ch = phys ^ SwzTile<D>::sw(row);
+    const int gr = min(row0 + row, rmax - 1);
+    __builtin_amdgcn_global_load_lds(src + (int64_t)gr * D + 8 * ch, (lds_void*)(dst + 8 * slot0), 16, 0, 0);
+  }
+}
+
+// Same for a vector of n <= 64 floats (one wave, 4 bytes per lane):
+// dst[i] = src[min(i, nmax - 1)].
+__device__ __forceinline__ void load_vec_lds(const float* __restrict__ src, int nmax, float* dst) {
+  const int l = threadIdx.x & 63;
+  __builtin_amdgcn_global_load_lds(src + min(l, nmax - 1), (lds_void*)dst, 4, 0, 0);
+}
+
+// Wait for this wave's outstanding global loads (incl. direct-to-LDS ones):
+// s_waitcnt vmcnt(0), leaving the LDS and export counters alone.
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 }  // namespace tt

@@ -32,15 +32,14 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(
     const u16* __restrict__ Q, const u16* __restrict__ K, const u16* __restrict__ V,
     u16* __restrict__ O, float* __restrict__ LSE, int Lq, int Lk, int BH, int nqt, int group,
     float sl2) {
+  using Tile = SwzTile<D>;
   constexpr int BM = FWD_BM, BN = FWD_BN;
-  constexpr int KP = D + 8;                   // sK pitch: 16-byte row reads, rows shift 4 banks
-  constexpr int VP = D == 32 ? 32 : D + 32;   // sV pitch: 4 rows of a transpose read hit 4 bank quarters
-  constexpr int NC = D / 16;                  // 16-wide k-chunks of the d contraction
-  constexpr int ND = D / 32;                  // 32-row tiles of O^T
-  constexpr int CPR = D / 8;                  // 16-byte chunks per row
-  constexpr int LPT = BN * CPR / 256;         // chunks per thread per tile
-  __shared__ __align__(16) u16 sK[BN * KP];
-  __shared__ __align__(16) u16 sV[BN * VP];
+  constexpr int NC = D / 16;  // 16-wide k-chunks of the d contraction
+  constexpr int ND = D / 32;  // 32-row tiles of O^T
+  constexpr int TE = Tile::kElems(BN);
+  // K and V tiles, double-buffered, filled by direct global->LDS loads
+  __shared__ __align__(16) u16 sK[2 * TE];
+  __shared__ __align__(16) u16 sV[2 * TE];
 
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, g = l >> 5, r32 = l & 31;
   int qt, bh;
@@ -74,34 +73,20 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(
   const int vcol = 16 * ((l >> 4) & 1) + 4 * (t16 & 3);
   const int vrow = 4 * g + (t16 >> 2);
 
-  uint4 kreg[LPT], vreg[LPT];
-  auto gload = [&](int kb) {
-#pragma unroll
-    for (int i = 0; i < LPT; ++i) {
-      const int c = tid + 256 * i;
-      const int key = min(kb + c / CPR, Lk - 1), ch = c % CPR;  // rows past Lk are masked
-      kreg[i] = ldg16(K + kbase + (int64_t)key * D + 8 * ch);
-      vreg[i] = ldg16(V + kbase + (int64_t)key * D + 8 * ch);
-    }
-  };
-  auto sstore = [&]() {
-#pragma unroll
-    for (int i = 0; i < LPT; ++i) {
-      const int c = tid + 256 * i;
-      const int key = c / CPR, ch = c % CPR;
-      *reinterpret_cast<uint4*>(&sK[key * KP + 8 * ch]) = kreg[i];
-      *reinterpret_cast<uint4*>(&sV[key * VP + 8 * ch]) = vreg[i];
-    }
+  // rows past Lk read row Lk - 1 and are masked
+  auto issue = [&](int kb, int buf) {
+    load_tile_lds<D, BN>(K + kbase, kb, Lk, sK + buf * TE);
+    load_tile_lds<D, BN>(V + kbase, kb, Lk, sV + buf * TE);
   };
 
-  auto tile = [&](int kb, auto mask_tag) {
+  auto tile = [&](int kb, const u16* tK, const u16* tV, auto mask_tag) {
     constexpr bool MASK = decltype(mask_tag)::value;
     f32x16 s[2] = {f32x16{}, f32x16{}};
 #pragma unroll
     for (int c = 0; c < NC; ++c)
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-        bf16x8 a = *reinterpret_cast<const bf16x8*>(&sK[(32 * t + r32) * KP + 16 * c + 8 * g]);
+        bf16x8 a = *reinterpret_cast<const bf16x8*>(&tK[Tile::chunk(32 * t + r32, 2 * c + g)]);
         s[t] = mfma_bf16_32x32x16(a, qf[c], s[t]);
       }
     if constexpr (MASK) {
@@ -153,24 +138,31 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(
     for (int kc = 0; kc < 4; ++kc)
 #pragma unroll
       for (int dt = 0; dt < ND; ++dt) {
-        const u16* p0 = &sV[(16 * kc + vrow) * VP + 32 * dt + vcol];
-        bf16x8 a = lds_read_tr16x2(p0, p0 + 8 * VP);
+        const int r0 = 16 * kc + vrow;
+        bf16x8 a = lds_read_tr16x2(&tV[Tile::at4(r0, 32 * dt + vcol)], &tV[Tile::at4(r0 + 8, 32 * dt + vcol)]);
         acc[dt] = mfma_bf16_32x32x16(a, pb[kc], acc[dt]);
       }
   };
 
-  if (kend > 0) gload(0);
-  for (int kb = 0; kb < kend; kb += BN) {
-    __syncthreads();
-    sstore();
-    __syncthreads();
-    if (kb + BN < kend) gload(kb + BN);
-    if (CAUSAL && kb > wq_hi) continue;  // every key of the tile is after every query of the wave
-    if ((kb + BN > Lk) || (CAUSAL && kb + BN - 1 > wq_lo))
-      tile(kb, std::true_type{});
-    else
-      tile(kb, std::false_type{});
-  }
+  // One barrier per tile: it publishes tile j (loaded during tile j-1) and
+  // retires every wave's reads of the other buffer before it is refilled.
+  // Tiles that need no mask run in their own loop, so neither loop branches
+  // between two register assignments of the accumulators.
+  int j = 0;
+  auto run = [&](int lo, int hi, auto mask_tag) {
+    for (int kb = lo; kb < hi; kb += BN, ++j) {
+      wait_vmem();
+      __syncthreads();
+      if (kb + BN < kend) issue(kb + BN, (j + 1) & 1);
+      if (CAUSAL && kb > wq_hi) continue;  // every key of the tile is after every query of the wave
+      tile(kb, sK + (j & 1) * TE, sV + (j & 1) * TE, mask_tag);
+    }
+  };
+  if (kend > 0) issue(0, 0);
+  // tiles below kfull lie entirely before the first query and inside Lk
+  const int kfull = CAUSAL ? min(q0, (Lk / BN) * BN) : (Lk / BN) * BN;
+  run(0, kfull, std::false_type{});
+  run(kfull, kend, std::true_type{});
 
   lsum += wave_xor32(lsum);
   if (qrow < Lq) {
