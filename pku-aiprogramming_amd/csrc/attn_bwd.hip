@@ -13,30 +13,45 @@
 //
 // Two kernels split the work so that every output row has one owner and no
 // atomics are needed:
-//   dkdv: workgroup = 128 keys (32 per wave, lane = key, K/V rows held in
-//         registers); loops over query tiles of 64 staged once in LDS.  The
-//         same LDS tile feeds the S / dP operands (16-byte row reads) and the
-//         transposed dV^T += dO^T P, dK^T += Q^T dS operands (gfx950
-//         transpose reads), so nothing is transposed on the way in.
-//   dq:   workgroup = 128 queries (lane = query, as in the forward); loops over
-//         key tiles of 64: S^T and dP^T from K / V row reads, dQ^T += K^T dS^T
-//         from transpose reads of the same K tile.
-// Loads past the end of a sequence read a clamped (valid) row and the
-// result is masked, so the inner loops carry no load guards.
+//   dkdv: workgroup = NW waves x 32 keys (lane = key; K rows in registers, V
+//         rows in LDS); loops over query tiles that stream through a
+//         STAGES-deep ring of LDS buffers.  The same tile feeds the S / dP
+//         operands (16-byte row reads) and the transposed
+//         dV^T += dO^T P, dK^T += Q^T dS operands (gfx950 transpose reads).
+//   dq:   workgroup = NW waves x 32 queries (lane = query, as the forward);
+//         loops over key tiles: S^T and dP^T from K / V row reads,
+//         dQ^T += K^T dS^T from transpose reads of the same K tile.
+// All tiles are filled by direct global->LDS loads.  Loads past the end of a
+// sequence read a clamped (valid) row and the result is masked, so the
+// inner loops carry no load guards.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
 #include <type_traits>
 
+#include "attn_bwd_f32.h"
 #include "attn_common.h"
 #include "attn_tiles.h"
 
 namespace tt {
 
-constexpr int DKDV_BN = 128;  // keys per workgroup
-constexpr int DKDV_BQ = 64;   // queries per LDS step (fp32 kernel)
-constexpr int DQ_BM = 128;    // queries per workgroup
-constexpr int DQ_BN = 64;     // keys per LDS step
+// Waves per workgroup, pipeline depth, and tile sizes of the bf16 kernels.
+// Default: 4-wave workgroups with 2 stages, so two workgroups with
+// independent barriers share each CU (2 waves per SIMD); measured faster on
+// the MI355X than one 8-wave workgroup with a 4-deep ring.
+#ifndef TT_BWD_WAVES
+#define TT_BWD_WAVES 4
+#endif
+#ifndef TT_BWD_STAGES
+#define TT_BWD_STAGES 2
+#endif
+constexpr int bwd_nw(int D) { return D == 32 ? 4 : TT_BWD_WAVES; }
+constexpr int kBwdStages = TT_BWD_STAGES;
+static_assert(kBwdStages >= 2 && kBwdStages <= 4, "tile ring depth must be 2..4");
+constexpr int DQ_BN = 64;  // keys per LDS tile of the dQ kernel
+// Query rows per LDS tile of the dK/dV kernel: the ring of Q / dO tiles
+// plus the V rows of the workgroup fit 160 KB of LDS.
+constexpr int dkdv_bq(int D) { return D == 128 ? 32 : 64; }
 
 // D_i = sum_d dO[i][d] * O[i][d], one 16-byte chunk per thread; also
 // L2_i = LSE_i * log2(e), the log-sum-exp in the log2 domain the MFMA
@@ -77,31 +92,27 @@ __global__ __launch_bounds__(256) void attn_bwd_delta_kernel(const T* __restrict
 }
 
 // ------------------------------------------------------------------ bf16 dK, dV
-// Query rows per LDS step of the dK/dV kernel: 32 at d = 128 keeps the
-// double-buffered Q / dO tiles plus the V tile at 64.5 KB, so two
-// workgroups (2 waves per SIMD) share a CU.
-constexpr int dkdv_bq(int D) { return D == 128 ? 32 : 64; }
-
 template <int D, bool CAUSAL>
-__global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_bf16_kernel(
+__global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_bf16_kernel(
     const u16* __restrict__ Q, const u16* __restrict__ K, const u16* __restrict__ V,
     const u16* __restrict__ dO, const float* __restrict__ L2, const float* __restrict__ Delta,
     u16* __restrict__ dK, u16* __restrict__ dV, int Lq, int Lk, int BH, int nkt, int group, float sl2,
     float scale) {
   using Tile = SwzTile<D>;
-  constexpr int BN = DKDV_BN, BQ = dkdv_bq(D), MT = BQ / 32;
+  constexpr int NW = bwd_nw(D), BN = 32 * NW, BQ = dkdv_bq(D), MT = BQ / 32, S = kBwdStages;
   constexpr int NC = D / 16, ND = D / 32;
   constexpr int TE = Tile::kElems(BQ);
   constexpr int VS = 64;  // stride of the LSE / D row buffers (one 64-lane load each)
-  // Q / dO tiles and their LSE (log2) / D rows, double-buffered, and the
-  // workgroup's V rows, all filled by direct global->LDS loads
-  __shared__ __align__(16) u16 sQ[2 * TE];
-  __shared__ __align__(16) u16 sdO[2 * TE];
+  constexpr int IPT = 2 * tile_loads<D, BQ, NW>();  // Q + dO loads per wave per tile
+  // Ring of Q / dO tiles with their LSE (log2) / D rows, and the workgroup's
+  // V rows, all filled by direct global->LDS loads
+  __shared__ __align__(16) u16 sQ[S * TE];
+  __shared__ __align__(16) u16 sdO[S * TE];
   __shared__ __align__(16) u16 sV[Tile::kElems(BN)];
-  __shared__ __align__(16) float sL[2 * VS];
-  __shared__ __align__(16) float sDl[2 * VS];
+  __shared__ __align__(16) float sL[S * VS];
+  __shared__ __align__(16) float sDl[S * VS];
 
-  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, g = l >> 5, r32 = l & 31;
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63, g = l >> 5, r32 = l & 31;
   int kt, bh;
   map_tile(blockIdx.x, nkt, BH, group, kt, bh, false);  // causal: key tile 0 sees every query
   const int k0 = kt * BN;
@@ -118,7 +129,6 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_bf16_kernel(
     for (int c = 0; c < NC; ++c)
       kf[c] = __builtin_bit_cast(bf16x8, ldg16(K + kbase + (int64_t)kr * D + 16 * c + 8 * g));
   }
-  load_tile_lds<D, BN>(V + kbase, k0, Lk, sV);  // published by the first loop barrier
   f32x16 adk[ND], adv[ND];
 #pragma unroll
   for (int dt = 0; dt < ND; ++dt) adk[dt] = adv[dt] = f32x16{};
@@ -128,13 +138,21 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_bf16_kernel(
   const int trow = 4 * g + (t16 >> 2);
   const int tcol = 16 * ((l >> 4) & 1) + 4 * (t16 & 3);
 
+  // Tile ring over query tiles [qstart, Lq): tile n lives in buffer n % S.
   // Query rows past Lq read row Lq - 1 and are masked (P = 0) in the edge step.
-  auto issue = [&](int qb, int buf) {
-    load_tile_lds<D, BQ>(Q + qbase, qb, Lq, sQ + buf * TE);
-    load_tile_lds<D, BQ>(dO + qbase, qb, Lq, sdO + buf * TE);
-    if (w == 0) {
-      load_vec_lds(L2 + lbase + qb, Lq - qb, sL + buf * VS);
-      load_vec_lds(Delta + lbase + qb, Lq - qb, sDl + buf * VS);
+  const int qstart = CAUSAL ? k0 : 0;  // k0 is a multiple of BQ
+  const int ntiles = Lq > qstart ? (Lq - qstart + BQ - 1) / BQ : 0;
+  int issued = 0;
+  auto issue_next = [&]() {
+    if (issued < ntiles) {
+      const int b = issued % S, qb = qstart + issued * BQ;
+      load_tile_lds<D, BQ, NW>(Q + qbase, qb, Lq, sQ + b * TE);
+      load_tile_lds<D, BQ, NW>(dO + qbase, qb, Lq, sdO + b * TE);
+      if (w == 0) {
+        load_vec_lds(L2 + lbase + qb, Lq - qb, sL + b * VS);
+        load_vec_lds(Delta + lbase + qb, Lq - qb, sDl + b * VS);
+      }
+      ++issued;
     }
   };
 
@@ -150,6 +168,12 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_bf16_kernel(
         const bf16x8 vb = *reinterpret_cast<const bf16x8*>(&sV[Tile::chunk(32 * w + r32, 2 * c + g)]);
         dp = mfma_bf16_32x32x16(*reinterpret_cast<const bf16x8*>(&tdO[off]), vb, dp);
       }
+      // transposed dO / Q operands of dV^T / dK^T MFMA i = h * ND + dt (no
+      // look-ahead here: at d = 128 the extra registers spill)
+      auto tr_op = [&](const u16* tile_, int i) {
+        const int r0 = 32 * mt + 16 * (i / ND) + trow, col = 32 * (i % ND) + tcol;
+        return lds_read_tr16x2(&tile_[Tile::at4(r0, col)], &tile_[Tile::at4(r0 + 8, col)]);
+      };
       // s[r] = S[query qb + 32mt + acc_row(r, g)][key]
       bf16x8 pb[2], db[2];
 #pragma unroll
@@ -174,37 +198,40 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_bf16_kernel(
       // dV^T += dO^T P and dK^T += Q^T dS over the 32 queries of this half:
       // k-chunk h holds queries 32mt + 16h + perm16 order.
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int dt = 0; dt < ND; ++dt) {
-          const int r0 = 32 * mt + 16 * h + trow;
-          const int o0 = Tile::at4(r0, 32 * dt + tcol), o1 = Tile::at4(r0 + 8, 32 * dt + tcol);
-          adv[dt] = mfma_bf16_32x32x16(lds_read_tr16x2(&tdO[o0], &tdO[o1]), pb[h], adv[dt]);
-          adk[dt] = mfma_bf16_32x32x16(lds_read_tr16x2(&tQ[o0], &tQ[o1]), db[h], adk[dt]);
-        }
+      for (int i = 0; i < 2 * ND; ++i) {
+        adv[i % ND] = mfma_bf16_32x32x16(tr_op(tdO, i), pb[i / ND], adv[i % ND]);
+        adk[i % ND] = mfma_bf16_32x32x16(tr_op(tQ, i), db[i / ND], adk[i % ND]);
+      }
     }
   };
 
-  // Masked (diagonal / ragged) and unmasked query tiles run in separate
-  // loops so that neither loop switches the accumulators' registers.
+  // One barrier per tile (see the forward kernel).  Masked (diagonal /
+  // ragged) and unmasked query tiles run in separate loops so that neither
+  // loop switches the accumulators' registers.
   int j = 0;
   auto run = [&](int lo, int hi, auto mask_tag) {
     for (int qb = lo; qb < hi; qb += BQ, ++j) {
-      wait_vmem();
-      __syncthreads();  // publishes tile j, retires all reads of the buffer refilled next
-      if (qb + BQ < Lq) issue(qb + BQ, (j + 1) & 1);
+      if (w == 0)
+        wait_vmem_tiles<IPT + 2>(issued - 1 - j);
+      else
+        wait_vmem_tiles<IPT>(issued - 1 - j);
+      __syncthreads();
+      issue_next();
       if (CAUSAL && qb + BQ - 1 < wk_lo) continue;  // every query of the tile precedes every key of the wave
-      const int b = j & 1;
+      const int b = j % S;
       step(qb, sQ + b * TE, sdO + b * TE, sL + b * VS, sDl + b * VS, mask_tag);
     }
   };
-  const int qstart = CAUSAL ? k0 : 0;  // k0 is a multiple of BQ
-  if (qstart < Lq) issue(qstart, 0);
+  // The V tile is issued first, so the first wait (which leaves at most the
+  // later Q / dO tiles outstanding) also covers it.
+  load_tile_lds<D, BN, NW>(V + kbase, k0, Lk, sV);
+  for (int s0 = 0; s0 < S - 1; ++s0) issue_next();
   const int qfull = (Lq / BQ) * BQ;
   const int qdiag = CAUSAL ? min(k0 + BN, Lq) : qstart;  // [qstart, qdiag): tiles crossing the diagonal
   run(qstart, qdiag, std::true_type{});
   run(qdiag, qfull, std::false_type{});
   run(max(qdiag, qfull), Lq, std::true_type{});
+  wait_vmem_le<0>();  // nothing may be in flight into LDS when the workgroup exits
 
   if (key < Lk) {
     u16* dkrow = dK + kbase + (int64_t)key * D;
@@ -227,19 +254,20 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_bf16_kernel(
 
 // ------------------------------------------------------------------ bf16 dQ
 template <int D, bool CAUSAL>
-__global__ __launch_bounds__(256, 2) void attn_bwd_dq_bf16_kernel(
+__global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dq_bf16_kernel(
     const u16* __restrict__ Q, const u16* __restrict__ K, const u16* __restrict__ V,
     const u16* __restrict__ dO, const float* __restrict__ L2, const float* __restrict__ Delta,
     u16* __restrict__ dQ, int Lq, int Lk, int BH, int nqt, int group, float sl2, float scale) {
   using Tile = SwzTile<D>;
-  constexpr int BM = DQ_BM, BN = DQ_BN;
+  constexpr int NW = bwd_nw(D), BM = 32 * NW, BN = DQ_BN, S = kBwdStages;
   constexpr int NC = D / 16, ND = D / 32;
   constexpr int TE = Tile::kElems(BN);
-  // K / V tiles, double-buffered, filled by direct global->LDS loads
-  __shared__ __align__(16) u16 sK[2 * TE];
-  __shared__ __align__(16) u16 sV[2 * TE];
+  constexpr int IPT = 2 * tile_loads<D, BN, NW>();  // K + V loads per wave per tile
+  // rings of K / V tiles filled by direct global->LDS loads
+  __shared__ __align__(16) u16 sK[S * TE];
+  __shared__ __align__(16) u16 sV[S * TE];
 
-  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, g = l >> 5, r32 = l & 31;
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63, g = l >> 5, r32 = l & 31;
   int qt, bh;
   map_tile(blockIdx.x, nqt, BH, group, qt, bh, CAUSAL);
   const int q0 = qt * BM;
@@ -268,23 +296,46 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_bf16_kernel(
   const int trow = 4 * g + (t16 >> 2);
   const int tcol = 16 * ((l >> 4) & 1) + 4 * (t16 & 3);
 
-  // key rows past Lk read row Lk - 1 and are masked (P = 0) in the edge tile
-  auto issue = [&](int kb, int buf) {
-    load_tile_lds<D, BN>(K + kbase, kb, Lk, sK + buf * TE);
-    load_tile_lds<D, BN>(V + kbase, kb, Lk, sV + buf * TE);
+  // Tile ring over key tiles; rows past Lk read row Lk - 1 and are masked.
+  const int kend = CAUSAL ? min(Lk, q0 + BM) : Lk;
+  const int ntiles = (kend + BN - 1) / BN;
+  int issued = 0;
+  auto issue_next = [&]() {
+    if (issued < ntiles) {
+      const int b = issued % S;
+      load_tile_lds<D, BN, NW>(K + kbase, issued * BN, Lk, sK + b * TE);
+      load_tile_lds<D, BN, NW>(V + kbase, issued * BN, Lk, sV + b * TE);
+      ++issued;
+    }
   };
 
   auto tile = [&](int kb, const u16* tK, const u16* tV, auto mask_tag) {
     constexpr bool MASK = decltype(mask_tag)::value;
+    // Operand fetches run one step ahead of the MFMAs that consume them.
+    auto kv_row = [&](const u16* tile_, int t, int c) {
+      return *reinterpret_cast<const bf16x8*>(&tile_[Tile::chunk(32 * t + r32, 2 * c + g)]);
+    };
+    auto kt_op = [&](int t, int i) {  // K^T operand of dQ^T MFMA i = h * ND + dt
+      const int r0 = 32 * t + 16 * (i / ND) + trow, col = 32 * (i % ND) + tcol;
+      return lds_read_tr16x2(&tK[Tile::at4(r0, col)], &tK[Tile::at4(r0 + 8, col)]);
+    };
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       f32x16 s = f32x16{}, dp = f32x16{};
+      bf16x8 ka[2], va[2];
+      ka[0] = kv_row(tK, t, 0);
+      va[0] = kv_row(tV, t, 0);
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
-        const int off = Tile::chunk(32 * t + r32, 2 * c + g);
-        s = mfma_bf16_32x32x16(*reinterpret_cast<const bf16x8*>(&tK[off]), qf[c], s);
-        dp = mfma_bf16_32x32x16(*reinterpret_cast<const bf16x8*>(&tV[off]), dof[c], dp);
+        if (c + 1 < NC) {
+          ka[(c + 1) & 1] = kv_row(tK, t, c + 1);
+          va[(c + 1) & 1] = kv_row(tV, t, c + 1);
+        }
+        s = mfma_bf16_32x32x16(ka[c & 1], qf[c], s);
+        dp = mfma_bf16_32x32x16(va[c & 1], dof[c], dp);
       }
+      bf16x8 qa[2];
+      qa[0] = kt_op(t, 0);  // in flight during the softmax
       bf16x8 db[2];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
@@ -296,28 +347,25 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_bf16_kernel(
         db[r >> 3][r & 7] = (__bf16)(p * (dp[r] - dl));
       }
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int dt = 0; dt < ND; ++dt) {
-          const int r0 = 32 * t + 16 * h + trow;
-          const bf16x8 a = lds_read_tr16x2(&tK[Tile::at4(r0, 32 * dt + tcol)], &tK[Tile::at4(r0 + 8, 32 * dt + tcol)]);
-          adq[dt] = mfma_bf16_32x32x16(a, db[h], adq[dt]);
-        }
+      for (int i = 0; i < 2 * ND; ++i) {
+        if (i + 1 < 2 * ND) qa[(i + 1) & 1] = kt_op(t, i + 1);
+        adq[i % ND] = mfma_bf16_32x32x16(qa[i & 1], db[i / ND], adq[i % ND]);
+      }
     }
   };
 
-  const int kend = CAUSAL ? min(Lk, q0 + BM) : Lk;
   int j = 0;
   auto run = [&](int lo, int hi, auto mask_tag) {
     for (int kb = lo; kb < hi; kb += BN, ++j) {
-      wait_vmem();
-      __syncthreads();  // publishes tile j, retires all reads of the buffer refilled next
-      if (kb + BN < kend) issue(kb + BN, (j + 1) & 1);
+      wait_vmem_tiles<IPT>(issued - 1 - j);
+      __syncthreads();
+      issue_next();
       if (CAUSAL && kb > wq_hi) continue;
-      tile(kb, sK + (j & 1) * TE, sV + (j & 1) * TE, mask_tag);
+      const int b = j % S;
+      tile(kb, sK + b * TE, sV + b * TE, mask_tag);
     }
   };
-  if (kend > 0) issue(0, 0);
+  for (int s0 = 0; s0 < S - 1; ++s0) issue_next();
   const int kfull = CAUSAL ? min(q0, (Lk / BN) * BN) : (Lk / BN) * BN;  // unmasked tiles
   run(0, kfull, std::false_type{});
   run(kfull, kend, std::true_type{});
@@ -332,239 +380,6 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_bf16_kernel(
         v.x = pack_bf16x2(adq[dt][r] * scale, adq[dt][r + 1] * scale);
         v.y = pack_bf16x2(adq[dt][r + 2] * scale, adq[dt][r + 3] * scale);
         *reinterpret_cast<uint2*>(row + 32 * dt + acc_row(r, g)) = v;
-      }
-  }
-}
-
-// ------------------------------------------------------------------ fp32 dK, dV
-// Same schedule on v_mfma_f32_32x32x2f32.  Each fp32 MFMA takes one k-value
-// per lane half, so the transposed operands are plain column reads of the
-// row-major tiles (consecutive lanes, consecutive columns).
-template <int D, bool CAUSAL>
-__global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_f32_kernel(
-    const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
-    const float* __restrict__ dO, const float* __restrict__ LSE, const float* __restrict__ Delta,
-    float* __restrict__ dK, float* __restrict__ dV, int Lq, int Lk, int BH, int nkt, int group,
-    float sl2, float scale) {
-  constexpr int BN = DKDV_BN, BQ = DKDV_BQ;
-  constexpr int P = D + 1;
-  constexpr int NC = D / 2, ND = D / 32, CPR = D / 4;
-  constexpr int LPT = BQ * CPR / 256;
-  __shared__ float sQ[BQ * P];
-  __shared__ float sdO[BQ * P];
-  __shared__ float sL[BQ];
-  __shared__ float sDl[BQ];
-
-  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, g = l >> 5, r32 = l & 31;
-  int kt, bh;
-  map_tile(blockIdx.x, nkt, BH, group, kt, bh, false);
-  const int k0 = kt * BN;
-  const int key = k0 + 32 * w + r32;
-  const int wk_lo = k0 + 32 * w;
-  const int64_t qbase = (int64_t)bh * Lq * D;
-  const int64_t kbase = (int64_t)bh * Lk * D;
-  const int64_t lbase = (int64_t)bh * Lq;
-
-  float kf[NC], vf[NC];
-  {
-    const int kr = min(key, Lk - 1);
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      kf[c] = K[kbase + (int64_t)kr * D + 2 * c + g];
-      vf[c] = V[kbase + (int64_t)kr * D + 2 * c + g];
-    }
-  }
-  f32x16 adk[ND], adv[ND];
-#pragma unroll
-  for (int dt = 0; dt < ND; ++dt) adk[dt] = adv[dt] = f32x16{};
-
-  float4 qreg[LPT], oreg[LPT];
-  float lreg = 0.f, dreg = 0.f;
-  auto gload = [&](int qb) {
-#pragma unroll
-    for (int i = 0; i < LPT; ++i) {
-      const int c = tid + 256 * i;
-      const int row = min(qb + c / CPR, Lq - 1), ch = c % CPR;
-      qreg[i] = *reinterpret_cast<const float4*>(Q + qbase + (int64_t)row * D + 4 * ch);
-      oreg[i] = *reinterpret_cast<const float4*>(dO + qbase + (int64_t)row * D + 4 * ch);
-    }
-    if (tid < BQ) {
-      const bool in = qb + tid < Lq;
-      lreg = in ? LSE[lbase + qb + tid] * kLog2e : INFINITY;
-      dreg = in ? Delta[lbase + qb + tid] : 0.f;
-    }
-  };
-  auto sstore = [&]() {
-#pragma unroll
-    for (int i = 0; i < LPT; ++i) {
-      const int c = tid + 256 * i;
-      const int row = c / CPR, ch = c % CPR;
-      float* pq = &sQ[row * P + 4 * ch];
-      float* po = &sdO[row * P + 4 * ch];
-      pq[0] = qreg[i].x; pq[1] = qreg[i].y; pq[2] = qreg[i].z; pq[3] = qreg[i].w;
-      po[0] = oreg[i].x; po[1] = oreg[i].y; po[2] = oreg[i].z; po[3] = oreg[i].w;
-    }
-    if (tid < BQ) {
-      sL[tid] = lreg;
-      sDl[tid] = dreg;
-    }
-  };
-
-  const int qstart = CAUSAL ? (k0 / BQ) * BQ : 0;
-  if (qstart < Lq) gload(qstart);
-  for (int qb = qstart; qb < Lq; qb += BQ) {
-    __syncthreads();
-    sstore();
-    __syncthreads();
-    if (qb + BQ < Lq) gload(qb + BQ);
-    if (CAUSAL && qb + BQ - 1 < wk_lo) continue;
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      f32x16 s = f32x16{}, dp = f32x16{};
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        s = mfma_f32_32x32x2(sQ[(32 * mt + r32) * P + 2 * c + g], kf[c], s);
-        dp = mfma_f32_32x32x2(sdO[(32 * mt + r32) * P + 2 * c + g], vf[c], dp);
-      }
-      const bool need_mask = CAUSAL && (qb + 32 * mt < wk_lo + 31);
-      float pr[16], dsr[16];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int qi = 32 * mt + acc_row(r, g);
-        float p = fast_exp2(fmaf(s[r], sl2, -sL[qi]));
-        if (need_mask && key > qb + qi) p = 0.f;
-        pr[r] = p;
-        dsr[r] = p * (dp[r] - sDl[qi]);
-      }
-#pragma unroll
-      for (int dt = 0; dt < ND; ++dt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int qi = 32 * mt + acc_row(r, g);
-          adv[dt] = mfma_f32_32x32x2(sdO[qi * P + 32 * dt + r32], pr[r], adv[dt]);
-          adk[dt] = mfma_f32_32x32x2(sQ[qi * P + 32 * dt + r32], dsr[r], adk[dt]);
-        }
-    }
-  }
-
-  if (key < Lk) {
-    float* dkrow = dK + kbase + (int64_t)key * D;
-    float* dvrow = dV + kbase + (int64_t)key * D;
-#pragma unroll
-    for (int dt = 0; dt < ND; ++dt)
-#pragma unroll
-      for (int r = 0; r < 16; r += 4) {
-        const int d0 = 32 * dt + acc_row(r, g);
-        float4 a = {adk[dt][r] * scale, adk[dt][r + 1] * scale, adk[dt][r + 2] * scale, adk[dt][r + 3] * scale};
-        float4 b = {adv[dt][r], adv[dt][r + 1], adv[dt][r + 2], adv[dt][r + 3]};
-        *reinterpret_cast<float4*>(dkrow + d0) = a;
-        *reinterpret_cast<float4*>(dvrow + d0) = b;
-      }
-  }
-}
-
-// ------------------------------------------------------------------ fp32 dQ
-template <int D, bool CAUSAL>
-__global__ __launch_bounds__(256, 1) void attn_bwd_dq_f32_kernel(
-    const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
-    const float* __restrict__ dO, const float* __restrict__ LSE, const float* __restrict__ Delta,
-    float* __restrict__ dQ, int Lq, int Lk, int BH, int nqt, int group, float sl2, float scale) {
-  constexpr int BM = DQ_BM, BN = DQ_BN;
-  constexpr int P = D + 1;
-  constexpr int NC = D / 2, ND = D / 32, CPR = D / 4;
-  constexpr int LPT = BN * CPR / 256;
-  __shared__ float sK[BN * P];
-  __shared__ float sV[BN * P];
-
-  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, g = l >> 5, r32 = l & 31;
-  int qt, bh;
-  map_tile(blockIdx.x, nqt, BH, group, qt, bh, CAUSAL);
-  const int q0 = qt * BM;
-  const int qrow = q0 + 32 * w + r32;
-  const int wq_lo = q0 + 32 * w, wq_hi = wq_lo + 31;
-  const int64_t qbase = (int64_t)bh * Lq * D;
-  const int64_t kbase = (int64_t)bh * Lk * D;
-
-  float qf[NC], dof[NC];
-  {
-    const int qr = min(qrow, Lq - 1);
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      qf[c] = Q[qbase + (int64_t)qr * D + 2 * c + g];
-      dof[c] = dO[qbase + (int64_t)qr * D + 2 * c + g];
-    }
-  }
-  const float lse2 = qrow < Lq ? LSE[(int64_t)bh * Lq + qrow] * kLog2e : INFINITY;
-  const float dl = qrow < Lq ? Delta[(int64_t)bh * Lq + qrow] : 0.f;
-  f32x16 adq[ND];
-#pragma unroll
-  for (int dt = 0; dt < ND; ++dt) adq[dt] = f32x16{};
-
-  float4 kreg[LPT], vreg[LPT];
-  auto gload = [&](int kb) {
-#pragma unroll
-    for (int i = 0; i < LPT; ++i) {
-      const int c = tid + 256 * i;
-      const int row = min(kb + c / CPR, Lk - 1), ch = c % CPR;
-      kreg[i] = *reinterpret_cast<const float4*>(K + kbase + (int64_t)row * D + 4 * ch);
-      vreg[i] = *reinterpret_cast<const float4*>(V + kbase + (int64_t)row * D + 4 * ch);
-    }
-  };
-  auto sstore = [&]() {
-#pragma unroll
-    for (int i = 0; i < LPT; ++i) {
-      const int c = tid + 256 * i;
-      const int row = c / CPR, ch = c % CPR;
-      float* pk = &sK[row * P + 4 * ch];
-      float* pv = &sV[row * P + 4 * ch];
-      pk[0] = kreg[i].x; pk[1] = kreg[i].y; pk[2] = kreg[i].z; pk[3] = kreg[i].w;
-      pv[0] = vreg[i].x; pv[1] = vreg[i].y; pv[2] = vreg[i].z; pv[3] = vreg[i].w;
-    }
-  };
-
-  const int kend = CAUSAL ? min(Lk, q0 + BM) : Lk;
-  if (kend > 0) gload(0);
-  for (int kb = 0; kb < kend; kb += BN) {
-    __syncthreads();
-    sstore();
-    __syncthreads();
-    if (kb + BN < kend) gload(kb + BN);
-    if (CAUSAL && kb > wq_hi) continue;
-    const bool need_mask = (kb + BN > Lk) || (CAUSAL && kb + BN - 1 > wq_lo);
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      f32x16 s = f32x16{}, dp = f32x16{};
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        s = mfma_f32_32x32x2(sK[(32 * t + r32) * P + 2 * c + g], qf[c], s);
-        dp = mfma_f32_32x32x2(sV[(32 * t + r32) * P + 2 * c + g], dof[c], dp);
-      }
-      float dsr[16];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float p = fast_exp2(fmaf(s[r], sl2, -lse2));
-        if (need_mask) {
-          const int kk = kb + 32 * t + acc_row(r, g);
-          if (kk >= Lk || (CAUSAL && kk > qrow)) p = 0.f;
-        }
-        dsr[r] = p * (dp[r] - dl);
-      }
-#pragma unroll
-      for (int dt = 0; dt < ND; ++dt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-          adq[dt] = mfma_f32_32x32x2(sK[(32 * t + acc_row(r, g)) * P + 32 * dt + r32], dsr[r], adq[dt]);
-    }
-  }
-
-  if (qrow < Lq) {
-    float* row = dQ + qbase + (int64_t)qrow * D;
-#pragma unroll
-    for (int dt = 0; dt < ND; ++dt)
-#pragma unroll
-      for (int r = 0; r < 16; r += 4) {
-        float4 v = {adq[dt][r] * scale, adq[dt][r + 1] * scale, adq[dt][r + 2] * scale, adq[dt][r + 3] * scale};
-        *reinterpret_cast<float4*>(row + 32 * dt + acc_row(r, g)) = v;
       }
   }
 }
@@ -588,18 +403,24 @@ static int launch_bwd(const T* q, const T* k, const T* v, const T* o, const floa
   TT_LAUNCHED("attention backward delta launch", st);
 
   const float sl2 = scale * kLog2e;
-  const int64_t nkt = (Lk + DKDV_BN - 1) / DKDV_BN;
-  const int64_t nqt = (Lq + DQ_BM - 1) / DQ_BM;
-  if (nkt * BH > 0x7fffffff || nqt * BH > 0x7fffffff) return fail(TT_ERR_ARG, "attention backward: grid too large");
-  const int gk = pick_group(BH, nkt, 32), gq = pick_group(BH, nqt, 32);
   if constexpr (BF) {
-    hipLaunchKernelGGL((attn_bwd_dkdv_bf16_kernel<D, CAUSAL>), dim3((unsigned)(nkt * BH)), dim3(256), 0, st,
+    constexpr int NW = bwd_nw(D);
+    const int64_t nkt = (Lk + 32 * NW - 1) / (32 * NW);
+    const int64_t nqt = (Lq + 32 * NW - 1) / (32 * NW);
+    if (nkt * BH > 0x7fffffff || nqt * BH > 0x7fffffff) return fail(TT_ERR_ARG, "attention backward: grid too large");
+    // heads in flight per XCD: tiles for the resident workgroups of its 32 CUs
+    const int gk = pick_group(BH, nkt, 32 * 8 / NW), gq = pick_group(BH, nqt, 32 * 8 / NW);
+    hipLaunchKernelGGL((attn_bwd_dkdv_bf16_kernel<D, CAUSAL>), dim3((unsigned)(nkt * BH)), dim3(64 * NW), 0, st,
                        q, k, v, dout, l2, delta, dk, dv, (int)Lq, (int)Lk, (int)BH, (int)nkt, gk, sl2, scale);
     TT_LAUNCHED("attention backward dK/dV launch", st);
-    hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<D, CAUSAL>), dim3((unsigned)(nqt * BH)), dim3(256), 0, st,
+    hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<D, CAUSAL>), dim3((unsigned)(nqt * BH)), dim3(64 * NW), 0, st,
                        q, k, v, dout, l2, delta, dq, (int)Lq, (int)Lk, (int)BH, (int)nqt, gq, sl2, scale);
     TT_LAUNCHED("attention backward dQ launch", st);
   } else {
+    const int64_t nkt = (Lk + BWD_F32_BN - 1) / BWD_F32_BN;
+    const int64_t nqt = (Lq + BWD_F32_BM - 1) / BWD_F32_BM;
+    if (nkt * BH > 0x7fffffff || nqt * BH > 0x7fffffff) return fail(TT_ERR_ARG, "attention backward: grid too large");
+    const int gk = pick_group(BH, nkt, 32), gq = pick_group(BH, nqt, 32);
     hipLaunchKernelGGL((attn_bwd_dkdv_f32_kernel<D, CAUSAL>), dim3((unsigned)(nkt * BH)), dim3(256), 0, st,
                        q, k, v, dout, lse, delta, dk, dv, (int)Lq, (int)Lk, (int)BH, (int)nkt, gk, sl2, scale);
     TT_LAUNCHED("attention backward dK/dV launch", st);

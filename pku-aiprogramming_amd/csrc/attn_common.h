@@ -126,22 +126,48 @@ typedef __attribute__((address_space(3))) void lds_void;
 // 256 threads take part; every wave instruction fills 64 consecutive 16-byte
 // LDS slots, each lane fetching the global chunk that belongs in its slot.
 // Completion: wait_vmem() then a barrier.
-template <int D, int ROWS>
+template <int D, int ROWS, int NW = 4>
 __device__ __forceinline__ void load_tile_lds(const u16* __restrict__ src, int row0, int rmax, u16* dst) {
   constexpr int CPR = D / 8;
-  constexpr int ITERS = ROWS * CPR / 256;
-  static_assert(ROWS * CPR % 256 == 0, "tile must be a whole number of 256-chunk rounds");
+  constexpr int CHUNKS = ROWS * CPR;
+  static_assert(CHUNKS % 64 == 0, "tile must be a whole number of 64-slot wave loads");
+  constexpr int ITERS = (CHUNKS + 64 * NW - 1) / (64 * NW);
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l = threadIdx.x & 63;
 #pragma unroll
   for (int i = 0; i < ITERS; ++i) {
-    const int slot0 = (i * 4 + w) * 64;  // first slot of this wave instruction (wave-uniform)
+    const int slot0 = (i * NW + w) * 64;  // first slot of this wave instruction (wave-uniform)
+    if (CHUNKS % (64 * NW) != 0 && slot0 >= CHUNKS) break;
     const int p = slot0 + l;
     const int row = p / CPR, phys = p % CPR;
     const int ch = phys ^ SwzTile<D>::sw(row);
     const int gr = min(row0 + row, rmax - 1);
     __builtin_amdgcn_global_load_lds(src + (int64_t)gr * D + 8 * ch, (lds_void*)(dst + 8 * slot0), 16, 0, 0);
   }
+}
+
+// Load instructions each wave issues per load_tile_lds call, for tiles that
+// split evenly over the NW waves (required where the count feeds a vmcnt wait).
+template <int D, int ROWS, int NW>
+constexpr int tile_loads() {
+  static_assert(ROWS * (D / 8) % (64 * NW) == 0, "tile must split evenly over the waves");
+  return ROWS * (D / 8) / (64 * NW);
+}
+
+// s_waitcnt vmcnt(N): wait until at most N of this wave's global loads are
+// outstanding (loads retire in order), LDS / export counters untouched.
+template <int N>
+__device__ __forceinline__ void wait_vmem_le() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+// Runtime count in [0, 3 * PER]: wait until at most n * PER loads remain.
+template <int PER>
+__device__ __forceinline__ void wait_vmem_tiles(int n) {
+  if (n >= 3) wait_vmem_le<3 * PER>();
+  else if (n == 2) wait_vmem_le<2 * PER>();
+  else if (n == 1) wait_vmem_le<PER>();
+  else wait_vmem_le<0>();
 }
 
 // Same for a vector of n <= 64 floats (one wave, 4 bytes per lane):

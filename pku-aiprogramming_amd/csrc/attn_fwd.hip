@@ -5,15 +5,17 @@
 // softmax order max -> sub -> exp -> sum -> div of src/Layers.cu:324-349)
 // with one kernel that never writes the L x L score matrix.
 //
-// Workgroup = 4 wavefronts = 128 queries of one (b, h); wave w owns queries
-// q0 + 32w .. q0 + 32w + 31, one per lane column.  K/V stream through LDS in
-// tiles of 64 keys; the next tile's global loads are issued before the MFMAs
-// of the current one.  Per tile and wave:
+// bf16 kernel: workgroup = NW wavefronts = 32*NW queries of one (b, h); wave
+// w owns queries q0 + 32w .. q0 + 32w + 31, one per lane column.  K/V tiles
+// of 64 keys stream through a STAGES-deep ring of LDS buffers filled by
+// direct global->LDS loads, so several tiles are in flight while one is
+// consumed.  Per tile and wave:
 //   S^T (64 keys x 32 queries) = K Q^T     (bf16 MFMA, Q held in registers)
 //   online softmax in the log2 domain      (running max m, running sum l)
-//   O^T (d x 32 queries) += V^T P^T        (P rounded to bf16, fp32 accum.)
-// The fp32 variant runs the same schedule on v_mfma_f32_32x32x2f32 with P kept
-// in fp32, which keeps the fp32 configs inside 1e-4.
+//   O^T (d x 32 queries) += V^T P^T        (P rounded to bf16, fp32 accum.;
+//                                           V^T read by LDS transpose reads)
+// The fp32 variant runs a simpler 2-stage schedule on v_mfma_f32_32x32x2f32
+// with P kept in fp32, which keeps the fp32 configs inside 1e-4.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -24,24 +26,37 @@
 
 namespace tt {
 
-constexpr int FWD_BM = 128;  // queries per workgroup
-constexpr int FWD_BN = 64;   // keys per LDS tile
+constexpr int FWD_BN = 64;  // keys per LDS tile
+// Waves per workgroup and pipeline depth (K/V tiles in flight) of the bf16
+// kernel.  Default: 4-wave workgroups with 2 stages (64 KB of LDS at
+// d = 128), so two workgroups with independent barriers share each CU.
+#ifndef TT_FWD_WAVES
+#define TT_FWD_WAVES 4
+#endif
+#ifndef TT_FWD_STAGES
+#define TT_FWD_STAGES 2
+#endif
+constexpr int fwd_nw(int D) { return D == 32 ? 4 : TT_FWD_WAVES; }
+constexpr int kStages = TT_FWD_STAGES;
+static_assert(kStages >= 2 && kStages <= 4, "K/V ring depth must be 2..4");
+constexpr int FWD_F32_BM = 128;  // queries per workgroup of the fp32 kernel
 
 template <int D, bool CAUSAL>
-__global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(
+__global__ __launch_bounds__(64 * fwd_nw(D), 8 / fwd_nw(D)) void attn_fwd_bf16_kernel(
     const u16* __restrict__ Q, const u16* __restrict__ K, const u16* __restrict__ V,
     u16* __restrict__ O, float* __restrict__ LSE, int Lq, int Lk, int BH, int nqt, int group,
     float sl2) {
   using Tile = SwzTile<D>;
-  constexpr int BM = FWD_BM, BN = FWD_BN;
+  constexpr int NW = fwd_nw(D), BM = 32 * NW, BN = FWD_BN, S = kStages;
   constexpr int NC = D / 16;  // 16-wide k-chunks of the d contraction
   constexpr int ND = D / 32;  // 32-row tiles of O^T
   constexpr int TE = Tile::kElems(BN);
-  // K and V tiles, double-buffered, filled by direct global->LDS loads
-  __shared__ __align__(16) u16 sK[2 * TE];
-  __shared__ __align__(16) u16 sV[2 * TE];
+  constexpr int IPT = 2 * tile_loads<D, BN, NW>();  // loads per wave per K+V tile
+  // K and V tiles, a ring of S buffers each
+  __shared__ __align__(16) u16 sK[S * TE];
+  __shared__ __align__(16) u16 sV[S * TE];
 
-  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, g = l >> 5, r32 = l & 31;
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63, g = l >> 5, r32 = l & 31;
   int qt, bh;
   map_tile(blockIdx.x, nqt, BH, group, qt, bh, CAUSAL);
   const int q0 = qt * BM;
@@ -53,10 +68,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(
   {
     const int qr = min(qrow, Lq - 1);  // padding rows read a valid row; never written back
 #pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      uint4 t = ldg16(Q + qbase + (int64_t)qr * D + 16 * c + 8 * g);
-      qf[c] = __builtin_bit_cast(bf16x8, t);
-    }
+    for (int c = 0; c < NC; ++c) qf[c] = __builtin_bit_cast(bf16x8, ldg16(Q + qbase + (int64_t)qr * D + 16 * c + 8 * g));
   }
 
   f32x16 acc[ND];
@@ -73,22 +85,47 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(
   const int vcol = 16 * ((l >> 4) & 1) + 4 * (t16 & 3);
   const int vrow = 4 * g + (t16 >> 2);
 
-  // rows past Lk read row Lk - 1 and are masked
-  auto issue = [&](int kb, int buf) {
-    load_tile_lds<D, BN>(K + kbase, kb, Lk, sK + buf * TE);
-    load_tile_lds<D, BN>(V + kbase, kb, Lk, sV + buf * TE);
+  // Tile ring: tile n lives in buffer n % S; rows past Lk read row Lk - 1
+  // and are masked.
+  const int ntiles = (kend + BN - 1) / BN;
+  int issued = 0;
+  auto issue_next = [&]() {
+    if (issued < ntiles) {
+      const int b = issued % S;
+      load_tile_lds<D, BN, NW>(K + kbase, issued * BN, Lk, sK + b * TE);
+      load_tile_lds<D, BN, NW>(V + kbase, issued * BN, Lk, sV + b * TE);
+      ++issued;
+    }
   };
 
   auto tile = [&](int kb, const u16* tK, const u16* tV, auto mask_tag) {
     constexpr bool MASK = decltype(mask_tag)::value;
+    // Operand fetches run one k-chunk ahead of the MFMAs that consume them,
+    // so LDS latency overlaps the previous chunk's MFMAs.
+    auto kread = [&](int c, int t) {
+      return *reinterpret_cast<const bf16x8*>(&tK[Tile::chunk(32 * t + r32, 2 * c + g)]);
+    };
+    auto vread = [&](int kc, int dt) {
+      const int r0 = 16 * kc + vrow;
+      return lds_read_tr16x2(&tV[Tile::at4(r0, 32 * dt + vcol)], &tV[Tile::at4(r0 + 8, 32 * dt + vcol)]);
+    };
     f32x16 s[2] = {f32x16{}, f32x16{}};
+    bf16x8 ka[2][2];
+    ka[0][0] = kread(0, 0);
+    ka[0][1] = kread(0, 1);
 #pragma unroll
-    for (int c = 0; c < NC; ++c)
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        bf16x8 a = *reinterpret_cast<const bf16x8*>(&tK[Tile::chunk(32 * t + r32, 2 * c + g)]);
-        s[t] = mfma_bf16_32x32x16(a, qf[c], s[t]);
+    for (int c = 0; c < NC; ++c) {
+      if (c + 1 < NC) {
+        ka[(c + 1) & 1][0] = kread(c + 1, 0);
+        ka[(c + 1) & 1][1] = kread(c + 1, 1);
       }
+      s[0] = mfma_bf16_32x32x16(ka[c & 1][0], qf[c], s[0]);
+      s[1] = mfma_bf16_32x32x16(ka[c & 1][1], qf[c], s[1]);
+    }
+    // first V^T operands, in flight during the softmax
+    bf16x8 va[2][ND];
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt) va[0][dt] = vread(0, dt);
     if constexpr (MASK) {
 #pragma unroll
       for (int t = 0; t < 2; ++t)
@@ -135,30 +172,33 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(
     // O^T += V^T P^T; chunk kc holds keys 16kc + perm16 order, read by two
     // transpose reads of 4 consecutive keys each.
 #pragma unroll
-    for (int kc = 0; kc < 4; ++kc)
+    for (int kc = 0; kc < 4; ++kc) {
+      if (kc + 1 < 4) {
 #pragma unroll
-      for (int dt = 0; dt < ND; ++dt) {
-        const int r0 = 16 * kc + vrow;
-        bf16x8 a = lds_read_tr16x2(&tV[Tile::at4(r0, 32 * dt + vcol)], &tV[Tile::at4(r0 + 8, 32 * dt + vcol)]);
-        acc[dt] = mfma_bf16_32x32x16(a, pb[kc], acc[dt]);
+        for (int dt = 0; dt < ND; ++dt) va[(kc + 1) & 1][dt] = vread(kc + 1, dt);
       }
+#pragma unroll
+      for (int dt = 0; dt < ND; ++dt) acc[dt] = mfma_bf16_32x32x16(va[kc & 1][dt], pb[kc], acc[dt]);
+    }
   };
 
-  // One barrier per tile: it publishes tile j (loaded during tile j-1) and
-  // retires every wave's reads of the other buffer before it is refilled.
-  // Tiles that need no mask run in their own loop, so neither loop branches
-  // between two register assignments of the accumulators.
+  // One barrier per tile: after this wave's loads of tile j have landed it
+  // publishes tile j to every wave and retires all reads of tile j - 1,
+  // whose buffer the next issue refills.  Tiles that need no mask run in
+  // their own loop, so neither loop branches between two register
+  // assignments of the accumulators.
   int j = 0;
   auto run = [&](int lo, int hi, auto mask_tag) {
     for (int kb = lo; kb < hi; kb += BN, ++j) {
-      wait_vmem();
+      wait_vmem_tiles<IPT>(issued - 1 - j);
       __syncthreads();
-      if (kb + BN < kend) issue(kb + BN, (j + 1) & 1);
+      issue_next();
       if (CAUSAL && kb > wq_hi) continue;  // every key of the tile is after every query of the wave
-      tile(kb, sK + (j & 1) * TE, sV + (j & 1) * TE, mask_tag);
+      const int b = j % S;
+      tile(kb, sK + b * TE, sV + b * TE, mask_tag);
     }
   };
-  if (kend > 0) issue(0, 0);
+  for (int s0 = 0; s0 < S - 1; ++s0) issue_next();
   // tiles below kfull lie entirely before the first query and inside Lk
   const int kfull = CAUSAL ? min(q0, (Lk / BN) * BN) : (Lk / BN) * BN;
   run(0, kfull, std::false_type{});
@@ -187,7 +227,7 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void attn_fwd_f32_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     float* __restrict__ O, float* __restrict__ LSE, int Lq, int Lk, int BH, int nqt, int group,
     float sl2) {
-  constexpr int BM = FWD_BM, BN = FWD_BN;
+  constexpr int BM = FWD_F32_BM, BN = FWD_BN;
   constexpr int P = D + 1;    // row pitch (floats): lanes on consecutive rows hit distinct banks
   constexpr int NC = D / 2;   // k-steps of the d contraction (2 per MFMA)
   constexpr int ND = D / 32;
@@ -205,8 +245,11 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void attn_fwd_f32_kernel(
   const int64_t kbase = (int64_t)bh * Lk * D;
 
   float qf[NC];
+  {
+    const int qr = min(qrow, Lq - 1);
 #pragma unroll
-  for (int c = 0; c < NC; ++c) qf[c] = (qrow < Lq) ? Q[qbase + (int64_t)qrow * D + 2 * c + g] : 0.f;
+    for (int c = 0; c < NC; ++c) qf[c] = Q[qbase + (int64_t)qr * D + 2 * c + g];
+  }
 
   f32x16 acc[ND];
 #pragma unroll
@@ -220,11 +263,9 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void attn_fwd_f32_kernel(
 #pragma unroll
     for (int i = 0; i < LPT; ++i) {
       const int c = tid + 256 * i;
-      const int key = c / CPR, ch = c % CPR;
-      float4 z = {0.f, 0.f, 0.f, 0.f};
-      const bool in = kb + key < Lk;
-      kreg[i] = in ? *reinterpret_cast<const float4*>(K + kbase + (int64_t)(kb + key) * D + 4 * ch) : z;
-      vreg[i] = in ? *reinterpret_cast<const float4*>(V + kbase + (int64_t)(kb + key) * D + 4 * ch) : z;
+      const int row = min(kb + c / CPR, Lk - 1), ch = c % CPR;  // rows past Lk are masked
+      kreg[i] = *reinterpret_cast<const float4*>(K + kbase + (int64_t)row * D + 4 * ch);
+      vreg[i] = *reinterpret_cast<const float4*>(V + kbase + (int64_t)row * D + 4 * ch);
     }
   };
   auto sstore = [&]() {
@@ -311,31 +352,46 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void attn_fwd_f32_kernel(
 }
 
 template <typename T, typename KernelPtr>
-static int launch_fwd(KernelPtr kern, const T* q, const T* k, const T* v, T* o, float* lse,
-                      int64_t BH, int64_t Lq, int64_t Lk, float scale, hipStream_t s) {
-  const int64_t nqt = (Lq + FWD_BM - 1) / FWD_BM;
+static int launch_fwd(KernelPtr kern, int bm, int threads, const T* q, const T* k, const T* v, T* o,
+                      float* lse, int64_t BH, int64_t Lq, int64_t Lk, float scale, hipStream_t s) {
+  const int64_t nqt = (Lq + bm - 1) / bm;
   const int64_t nblk = nqt * BH;
   if (nblk > 0x7fffffff) return fail(TT_ERR_ARG, "attention forward: grid too large");
-  const int group = pick_group(BH, nqt, 64);
-  hipLaunchKernelGGL(kern, dim3((unsigned)nblk), dim3(256), 0, s, q, k, v, o, lse, (int)Lq, (int)Lk,
+  // heads in flight per XCD: enough tiles for the resident workgroups of its
+  // 32 CUs (8 waves per CU: 2 per SIMD)
+  const int group = pick_group(BH, nqt, 32 * (512 / threads));
+  hipLaunchKernelGGL(kern, dim3((unsigned)nblk), dim3(threads), 0, s, q, k, v, o, lse, (int)Lq, (int)Lk,
                      (int)BH, (int)nqt, group, scale * kLog2e);
   TT_LAUNCHED("attention forward launch", s);
   return ok();
+}
+
+template <int D, bool CAUSAL>
+static int fwd_bf16(const u16* q, const u16* k, const u16* v, u16* o, float* lse, int64_t BH, int64_t Lq,
+                    int64_t Lk, float scale, hipStream_t st) {
+  constexpr int NW = fwd_nw(D);
+  return launch_fwd(attn_fwd_bf16_kernel<D, CAUSAL>, 32 * NW, 64 * NW, q, k, v, o, lse, BH, Lq, Lk, scale, st);
+}
+
+template <int D, bool CAUSAL>
+static int fwd_f32(const float* q, const float* k, const float* v, float* o, float* lse, int64_t BH, int64_t Lq,
+                   int64_t Lk, float scale, hipStream_t st) {
+  return launch_fwd(attn_fwd_f32_kernel<D, CAUSAL>, FWD_F32_BM, 256, q, k, v, o, lse, BH, Lq, Lk, scale, st);
 }
 
 }  // namespace tt
 
 using namespace tt;
 
-#define TT_FWD_DISPATCH(KERNEL, T)                                                              \
-  switch (d * 2 + (causal ? 1 : 0)) {                                                           \
-    case 64: return launch_fwd(KERNEL<32, false>, q, k, v, o, lse, BH, Lq, Lk, scale, st);      \
-    case 65: return launch_fwd(KERNEL<32, true>, q, k, v, o, lse, BH, Lq, Lk, scale, st);       \
-    case 128: return launch_fwd(KERNEL<64, false>, q, k, v, o, lse, BH, Lq, Lk, scale, st);     \
-    case 129: return launch_fwd(KERNEL<64, true>, q, k, v, o, lse, BH, Lq, Lk, scale, st);      \
-    case 256: return launch_fwd(KERNEL<128, false>, q, k, v, o, lse, BH, Lq, Lk, scale, st);    \
-    case 257: return launch_fwd(KERNEL<128, true>, q, k, v, o, lse, BH, Lq, Lk, scale, st);     \
-    default: return fail(TT_ERR_UNSUPPORTED, "attention forward: unsupported head dim");       \
+#define TT_FWD_DISPATCH(FN)                                                  \
+  switch (d * 2 + (causal ? 1 : 0)) {                                        \
+    case 64: return FN<32, false>(q, k, v, o, lse, BH, Lq, Lk, scale, st);   \
+    case 65: return FN<32, true>(q, k, v, o, lse, BH, Lq, Lk, scale, st);    \
+    case 128: return FN<64, false>(q, k, v, o, lse, BH, Lq, Lk, scale, st);  \
+    case 129: return FN<64, true>(q, k, v, o, lse, BH, Lq, Lk, scale, st);   \
+    case 256: return FN<128, false>(q, k, v, o, lse, BH, Lq, Lk, scale, st); \
+    case 257: return FN<128, true>(q, k, v, o, lse, BH, Lq, Lk, scale, st);  \
+    default: return fail(TT_ERR_UNSUPPORTED, "attention forward: unsupported head dim"); \
   }
 
 extern "C" int tt_attn_fwd_f32(const float* q, const float* k, const float* v, float* o, float* lse,
@@ -348,7 +404,7 @@ extern "C" int tt_attn_fwd_f32(const float* q, const float* k, const float* v, f
   if (!q || !k || !v || !o) return fail(TT_ERR_ARG, "tt_attn_fwd_f32: null pointer");
   if ((rc = ensure_init())) return rc;
   hipStream_t st = stream_or_default(stream);
-  TT_FWD_DISPATCH(attn_fwd_f32_kernel, float)
+  TT_FWD_DISPATCH(fwd_f32)
 }
 
 extern "C" int tt_attn_fwd_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o,
@@ -361,5 +417,5 @@ extern "C" int tt_attn_fwd_bf16(const uint16_t* q, const uint16_t* k, const uint
   if (!q || !k || !v || !o) return fail(TT_ERR_ARG, "tt_attn_fwd_bf16: null pointer");
   if ((rc = ensure_init())) return rc;
   hipStream_t st = stream_or_default(stream);
-  TT_FWD_DISPATCH(attn_fwd_bf16_kernel, u16)
+  TT_FWD_DISPATCH(fwd_bf16)
 }

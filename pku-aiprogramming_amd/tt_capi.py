@@ -19,7 +19,8 @@ import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 HEADER = os.path.join(os.path.dirname(HERE), "include", "tt_attn.h")
-LIB_PATH = os.path.join(HERE, "libtt_hip.so")
+# TT_LIB_PATH selects another build of the library (e.g. a tuning variant).
+LIB_PATH = os.environ.get("TT_LIB_PATH") or os.path.join(HERE, "libtt_hip.so")
 
 TT_OK, TT_ERR_ARG, TT_ERR_HIP, TT_ERR_UNSUPPORTED, TT_ERR_NOMEM = range(5)
 TT_F32, TT_F64, TT_I32, TT_BF16 = range(4)
