@@ -52,6 +52,15 @@ constexpr int DQ_BN = 64;  // keys per LDS tile of the dQ kernel
 // Query rows per LDS tile of the dK/dV kernel: the ring of Q / dO tiles
 // plus the V rows of the workgroup fit 160 KB of LDS.
 constexpr int dkdv_bq(int D) { return D == 128 ? 32 : 64; }
+// K chunks (16 columns each) the dK/dV kernel keeps in LDS rather than in
+// registers.  At d = 128 the dK / dV accumulators (128 VGPRs) and the K rows
+// (32) leave too little of the 256 registers of a 2-waves-per-SIMD kernel;
+// each parked chunk frees 4 VGPRs for one extra 16-byte LDS read per query
+// tile.
+#ifndef TT_DKDV_KLDS
+#define TT_DKDV_KLDS 3
+#endif
+constexpr int dkdv_klds(int D) { return D == 128 ? TT_DKDV_KLDS : 0; }
 
 // D_i = sum_d dO[i][d] * O[i][d], one 16-byte chunk per thread; also
 // L2_i = LSE_i * log2(e), the log-sum-exp in the log2 domain the MFMA
@@ -101,9 +110,12 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_b
   using Tile = SwzTile<D>;
   constexpr int NW = bwd_nw(D), BN = 32 * NW, BQ = dkdv_bq(D), MT = BQ / 32, S = kBwdStages;
   constexpr int NC = D / 16, ND = D / 32;
+  constexpr int KL = dkdv_klds(D), KR = NC - KL;  // K chunks parked in LDS / held in registers
+  static_assert(KL >= 0 && KL <= NC, "bad K chunk split");
   constexpr int TE = Tile::kElems(BQ);
   constexpr int VS = 64;  // stride of the LSE / D row buffers (one 64-lane load each)
-  constexpr int IPT = 2 * tile_loads<D, BQ, NW>();  // Q + dO loads per wave per tile
+  using Dma = TileDma<D, BQ, NW>;
+  constexpr int IPT = 2 * Dma::kLoads;  // Q + dO loads per wave per tile
   // Ring of Q / dO tiles with their LSE (log2) / D rows, and the workgroup's
   // V rows, all filled by direct global->LDS loads
   __shared__ __align__(16) u16 sQ[S * TE];
@@ -111,6 +123,8 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_b
   __shared__ __align__(16) u16 sV[Tile::kElems(BN)];
   __shared__ __align__(16) float sL[S * VS];
   __shared__ __align__(16) float sDl[S * VS];
+  // parked K chunks, lane-linear: chunk KR + c of lane l of wave w at 16 (64 (c NW + w) + l) bytes
+  __shared__ __align__(16) u16 sKf[(KL > 0 ? KL : 1) * NW * 512];
 
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63, g = l >> 5, r32 = l & 31;
   int kt, bh;
@@ -128,7 +142,13 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_b
 #pragma unroll
     for (int c = 0; c < NC; ++c)
       kf[c] = __builtin_bit_cast(bf16x8, ldg16(K + kbase + (int64_t)kr * D + 16 * c + 8 * g));
+#pragma unroll
+    for (int c = KR; c < NC; ++c) *reinterpret_cast<bf16x8*>(&sKf[((c - KR) * NW + w) * 512 + 8 * l]) = kf[c];
   }
+  // K operand of chunk c (each lane reads back only what it parked itself)
+  auto kop = [&](int c) {
+    return c < KR ? kf[c] : *reinterpret_cast<const bf16x8*>(&sKf[((c - KR) * NW + w) * 512 + 8 * l]);
+  };
   f32x16 adk[ND], adv[ND];
 #pragma unroll
   for (int dt = 0; dt < ND; ++dt) adk[dt] = adv[dt] = f32x16{};
@@ -142,12 +162,14 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_b
   // Query rows past Lq read row Lq - 1 and are masked (P = 0) in the edge step.
   const int qstart = CAUSAL ? k0 : 0;  // k0 is a multiple of BQ
   const int ntiles = Lq > qstart ? (Lq - qstart + BQ - 1) / BQ : 0;
+  Dma dma;
+  dma.init();
   int issued = 0;
   auto issue_next = [&]() {
     if (issued < ntiles) {
       const int b = issued % S, qb = qstart + issued * BQ;
-      load_tile_lds<D, BQ, NW>(Q + qbase, qb, Lq, sQ + b * TE);
-      load_tile_lds<D, BQ, NW>(dO + qbase, qb, Lq, sdO + b * TE);
+      dma.issue(Q + qbase, qb, Lq, sQ + b * TE);
+      dma.issue(dO + qbase, qb, Lq, sdO + b * TE);
       if (w == 0) {
         load_vec_lds(L2 + lbase + qb, Lq - qb, sL + b * VS);
         load_vec_lds(Delta + lbase + qb, Lq - qb, sDl + b * VS);
@@ -164,7 +186,7 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_b
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
         const int off = Tile::chunk(32 * mt + r32, 2 * c + g);
-        s = mfma_bf16_32x32x16(*reinterpret_cast<const bf16x8*>(&tQ[off]), kf[c], s);
+        s = mfma_bf16_32x32x16(*reinterpret_cast<const bf16x8*>(&tQ[off]), kop(c), s);
         const bf16x8 vb = *reinterpret_cast<const bf16x8*>(&sV[Tile::chunk(32 * w + r32, 2 * c + g)]);
         dp = mfma_bf16_32x32x16(*reinterpret_cast<const bf16x8*>(&tdO[off]), vb, dp);
       }
@@ -224,8 +246,16 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_b
   };
   // The V tile is issued first, so the first wait (which leaves at most the
   // later Q / dO tiles outstanding) also covers it.
-  load_tile_lds<D, BN, NW>(V + kbase, k0, Lk, sV);
+  {
+    TileDma<D, BN, NW> vdma;
+    vdma.init();
+    vdma.issue(V + kbase, k0, Lk, sV);
+  }
   for (int s0 = 0; s0 < S - 1; ++s0) issue_next();
+  // Retire the K row loads (and the first tiles with them) here: otherwise
+  // the compiler, which does not see the tile loads, keeps the K loads
+  // pending around the loop and waits for them on every iteration.
+  wait_vmem_le<0>();
   const int qfull = (Lq / BQ) * BQ;
   const int qdiag = CAUSAL ? min(k0 + BN, Lq) : qstart;  // [qstart, qdiag): tiles crossing the diagonal
   run(qstart, qdiag, std::true_type{});
@@ -262,7 +292,8 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dq_bf1
   constexpr int NW = bwd_nw(D), BM = 32 * NW, BN = DQ_BN, S = kBwdStages;
   constexpr int NC = D / 16, ND = D / 32;
   constexpr int TE = Tile::kElems(BN);
-  constexpr int IPT = 2 * tile_loads<D, BN, NW>();  // K + V loads per wave per tile
+  using Dma = TileDma<D, BN, NW>;
+  constexpr int IPT = 2 * Dma::kLoads;  // K + V loads per wave per tile
   // rings of K / V tiles filled by direct global->LDS loads
   __shared__ __align__(16) u16 sK[S * TE];
   __shared__ __align__(16) u16 sV[S * TE];
@@ -299,12 +330,14 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dq_bf1
   // Tile ring over key tiles; rows past Lk read row Lk - 1 and are masked.
   const int kend = CAUSAL ? min(Lk, q0 + BM) : Lk;
   const int ntiles = (kend + BN - 1) / BN;
+  Dma dma;
+  dma.init();
   int issued = 0;
   auto issue_next = [&]() {
     if (issued < ntiles) {
       const int b = issued % S;
-      load_tile_lds<D, BN, NW>(K + kbase, issued * BN, Lk, sK + b * TE);
-      load_tile_lds<D, BN, NW>(V + kbase, issued * BN, Lk, sV + b * TE);
+      dma.issue(K + kbase, issued * BN, Lk, sK + b * TE);
+      dma.issue(V + kbase, issued * BN, Lk, sV + b * TE);
       ++issued;
     }
   };
@@ -366,6 +399,7 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dq_bf1
     }
   };
   for (int s0 = 0; s0 < S - 1; ++s0) issue_next();
+  wait_vmem_le<0>();  // retire the Q / dO / LSE / D loads (see the dK/dV kernel)
   const int kfull = CAUSAL ? min(q0, (Lk / BN) * BN) : (Lk / BN) * BN;  // unmasked tiles
   run(0, kfull, std::false_type{});
   run(kfull, kend, std::true_type{});

@@ -102,7 +102,7 @@ __device__ __forceinline__ bool wave_any(bool p) { return __any(p); }
 //   D = 64  (two rows per line):   sw = (((r >> 1) & 1) << 2) | ((r >> 2) & 3)
 //   D = 32  (four rows per line):  sw = (r >> 2) & 3
 // The tile has no padding, so a wave's 64 consecutive 16-byte slots can be
-// filled by one direct global->LDS load (see load_tile_lds).
+// filled by one direct global->LDS load (see TileDma).
 template <int D>
 struct SwzTile {
   static constexpr int kCPR = D / 8;  // chunks per row
@@ -120,39 +120,80 @@ struct SwzTile {
 
 typedef __attribute__((address_space(3))) void lds_void;
 
-// Issue direct global->LDS loads (global_load_lds_dwordx4) of rows
-// [row0, row0 + ROWS) of a row-major [*, D] bf16 matrix into the SwzTile
-// `dst`.  Rows >= rmax read row rmax - 1 instead (callers mask them).  All
-// 256 threads take part; every wave instruction fills 64 consecutive 16-byte
-// LDS slots, each lane fetching the global chunk that belongs in its slot.
-// Completion: wait_vmem() then a barrier.
-template <int D, int ROWS, int NW = 4>
-__device__ __forceinline__ void load_tile_lds(const u16* __restrict__ src, int row0, int rmax, u16* dst) {
-  constexpr int CPR = D / 8;
-  constexpr int CHUNKS = ROWS * CPR;
-  static_assert(CHUNKS % 64 == 0, "tile must be a whole number of 64-slot wave loads");
-  constexpr int ITERS = (CHUNKS + 64 * NW - 1) / (64 * NW);
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int l = threadIdx.x & 63;
-#pragma unroll
-  for (int i = 0; i < ITERS; ++i) {
-    const int slot0 = (i * NW + w) * 64;  // first slot of this wave instruction (wave-uniform)
-    if (CHUNKS % (64 * NW) != 0 && slot0 >= CHUNKS) break;
-    const int p = slot0 + l;
-    const int row = p / CPR, phys = p % CPR;
-    const int ch = phys ^ SwzTile<D>::sw(row);
-    const int gr = min(row0 + row, rmax - 1);
-    __builtin_amdgcn_global_load_lds(src + (int64_t)gr * D + 8 * ch, (lds_void*)(dst + 8 * slot0), 16, 0, 0);
-  }
+// LDS byte address of a pointer into a __shared__ array.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const lds_void*)p;
 }
 
-// Load instructions each wave issues per load_tile_lds call, for tiles that
-// split evenly over the NW waves (required where the count feeds a vmcnt wait).
-template <int D, int ROWS, int NW>
-constexpr int tile_loads() {
-  static_assert(ROWS * (D / 8) % (64 * NW) == 0, "tile must split evenly over the waves");
-  return ROWS * (D / 8) / (64 * NW);
+// Direct global->LDS loads.  Lane l copies `bytes` bytes from
+// sbase + voff (sbase wave-uniform, voff per lane) to LDS byte address
+// lds + bytes * l; M0 carries the LDS base.
+//
+// They are written as inline asm on purpose.  The compiler's wait-count pass
+// does model the LDS write of the builtin form, but it cannot tell the
+// buffers of a tile ring apart (dynamic offsets into one array), so it puts
+// an s_waitcnt vmcnt(0) in front of the first LDS read of every tile, which
+// waits for the tile being prefetched and serialises the ring.  Here the
+// kernels order these loads themselves: a vmcnt wait for the tile (loads
+// retire in order) followed by a workgroup barrier, before any LDS read of
+// that buffer.  M0 is a reserved register that the compiler only sets right
+// before the instructions that read it; each statement sets it itself.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void glds16(const void* sbase, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds)
+               : "memory", "m0");
 }
+__device__ __forceinline__ void glds4(const void* sbase, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(sbase), "s"(lds)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// Direct global->LDS loader of [ROWS x D] bf16 tiles of a row-major [*, D]
+// matrix into SwzTile<D> buffers, shared by the NW waves of a workgroup.
+// Load instruction i of wave w fills the 64 consecutive 16-byte LDS slots
+// starting at slot 64 (i NW + w); each lane fetches the global chunk that
+// belongs in its slot.  One instruction covers 64 / kCPR rows, so step i
+// moves NW * 64 / kCPR rows on; every swizzle has a period dividing 16
+// rows, so when that step is a multiple of 16 the lane's chunk column is the
+// same for every i and the byte offset is voff + 1024 NW i, with voff
+// computed once.
+template <int D, int ROWS, int NW>
+struct TileDma {
+  static constexpr int kCPR = D / 8;
+  static_assert(ROWS * kCPR % (64 * NW) == 0, "tile must split evenly over the waves");
+  static_assert((NW * 64 / kCPR) % 16 == 0, "row step must keep the swizzle phase");
+  static constexpr int kLoads = ROWS * kCPR / (64 * NW);  // load instructions per wave per tile
+  uint32_t voff;  // this lane's byte offset for instruction 0, from the tile's first row
+  int w;
+
+  __device__ __forceinline__ void init() {
+    w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int p = w * 64 + (threadIdx.x & 63);
+    const int row = p / kCPR, ch = (p % kCPR) ^ SwzTile<D>::sw(row);
+    voff = 2u * (uint32_t)(row * D + 8 * ch);
+  }
+  // Issue the loads of rows [row0, row0 + ROWS) of `src` into the tile at
+  // `dst`.  Requires 0 <= row0 < rmax; rows >= rmax read row rmax - 1 instead
+  // (callers mask them).  Completion: a vmcnt wait, then a barrier.
+  __device__ __forceinline__ void issue(const u16* src, int row0, int rmax, const u16* dst) const {
+    const u16* base = src + (int64_t)row0 * D;
+    const uint32_t lds = lds_addr(dst) + 1024u * (uint32_t)w;
+    if (row0 + ROWS <= rmax) {
+#pragma unroll
+      for (int i = 0; i < kLoads; ++i) glds16(base + 512 * NW * i, voff, lds + 1024u * NW * i);
+    } else {
+      const int p0 = w * 64 + (threadIdx.x & 63);
+      const int r0 = p0 / kCPR, ch = (p0 % kCPR) ^ SwzTile<D>::sw(r0);
+#pragma unroll
+      for (int i = 0; i < kLoads; ++i) {
+        const int row = min(r0 + i * (NW * 64 / kCPR), rmax - 1 - row0);
+        glds16(base, 2u * (uint32_t)(row * D + 8 * ch), lds + 1024u * NW * i);
+      }
+    }
+  }
+};
 
 // s_waitcnt vmcnt(N): wait until at most N of this wave's global loads are
 // outstanding (loads retire in order), LDS / export counters untouched.
@@ -170,11 +211,16 @@ __device__ __forceinline__ void wait_vmem_tiles(int n) {
   else wait_vmem_le<0>();
 }
 
-// Same for a vector of n <= 64 floats (one wave, 4 bytes per lane):
-// dst[i] = src[min(i, nmax - 1)].
-__device__ __forceinline__ void load_vec_lds(const float* __restrict__ src, int nmax, float* dst) {
-  const int l = threadIdx.x & 63;
-  __builtin_amdgcn_global_load_lds(src + min(l, nmax - 1), (lds_void*)dst, 4, 0, 0);
+// Direct global->LDS load of 64 floats by one wave: dst[i] = src[min(i, nmax - 1)]
+// (src wave-uniform, nmax >= 1).
+__device__ __forceinline__ void load_vec_lds(const float* src, int nmax, const float* dst) {
+  // The lane index is recomputed here (volatile, so it is not hoisted out of
+  // the caller's loop): a register-starved kernel would otherwise keep it in
+  // a scratch slot, and the reload's vmcnt wait would drain the tile loads
+  // issued just before.
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  glds4(src, 4u * (uint32_t)min(l, nmax - 1), lds_addr(dst));
 }
 
 // Wait for this wave's outstanding global loads (incl. direct-to-LDS ones):

@@ -51,7 +51,8 @@ __global__ __launch_bounds__(64 * fwd_nw(D), 8 / fwd_nw(D)) void attn_fwd_bf16_k
   constexpr int NC = D / 16;  // 16-wide k-chunks of the d contraction
   constexpr int ND = D / 32;  // 32-row tiles of O^T
   constexpr int TE = Tile::kElems(BN);
-  constexpr int IPT = 2 * tile_loads<D, BN, NW>();  // loads per wave per K+V tile
+  using Dma = TileDma<D, BN, NW>;
+  constexpr int IPT = 2 * Dma::kLoads;  // loads per wave per K+V tile
   // K and V tiles, a ring of S buffers each
   __shared__ __align__(16) u16 sK[S * TE];
   __shared__ __align__(16) u16 sV[S * TE];
@@ -88,12 +89,14 @@ __global__ __launch_bounds__(64 * fwd_nw(D), 8 / fwd_nw(D)) void attn_fwd_bf16_k
   // Tile ring: tile n lives in buffer n % S; rows past Lk read row Lk - 1
   // and are masked.
   const int ntiles = (kend + BN - 1) / BN;
+  Dma dma;
+  dma.init();
   int issued = 0;
   auto issue_next = [&]() {
     if (issued < ntiles) {
       const int b = issued % S;
-      load_tile_lds<D, BN, NW>(K + kbase, issued * BN, Lk, sK + b * TE);
-      load_tile_lds<D, BN, NW>(V + kbase, issued * BN, Lk, sV + b * TE);
+      dma.issue(K + kbase, issued * BN, Lk, sK + b * TE);
+      dma.issue(V + kbase, issued * BN, Lk, sV + b * TE);
       ++issued;
     }
   };
@@ -199,6 +202,11 @@ __global__ __launch_bounds__(64 * fwd_nw(D), 8 / fwd_nw(D)) void attn_fwd_bf16_k
     }
   };
   for (int s0 = 0; s0 < S - 1; ++s0) issue_next();
+  // Retire the Q loads (and the first tiles with them) here: otherwise the
+  // compiler, which does not see the tile loads, keeps the Q loads pending
+  // around the loop and waits for them (and so for the prefetched tile) on
+  // every iteration.
+  wait_vmem_le<0>();
   // tiles below kfull lie entirely before the first query and inside Lk
   const int kfull = CAUSAL ? min(q0, (Lk / BN) * BN) : (Lk / BN) * BN;
   run(0, kfull, std::false_type{});
