@@ -190,8 +190,8 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_b
         const bf16x8 vb = *reinterpret_cast<const bf16x8*>(&sV[Tile::chunk(32 * w + r32, 2 * c + g)]);
         dp = mfma_bf16_32x32x16(*reinterpret_cast<const bf16x8*>(&tdO[off]), vb, dp);
       }
-      // transposed dO / Q operands of dV^T / dK^T MFMA i = h * ND + dt (no
-      // look-ahead here: at d = 128 the extra registers spill)
+      // transposed dO / Q operands of dV^T / dK^T MFMA i = h * ND + dt,
+      // fetched one MFMA pair ahead
       auto tr_op = [&](const u16* tile_, int i) {
         const int r0 = 32 * mt + 16 * (i / ND) + trow, col = 32 * (i % ND) + tcol;
         return lds_read_tr16x2(&tile_[Tile::at4(r0, col)], &tile_[Tile::at4(r0 + 8, col)]);
@@ -219,10 +219,17 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_b
       }
       // dV^T += dO^T P and dK^T += Q^T dS over the 32 queries of this half:
       // k-chunk h holds queries 32mt + 16h + perm16 order.
+      bf16x8 ov[2], oq[2];
+      ov[0] = tr_op(tdO, 0);
+      oq[0] = tr_op(tQ, 0);
 #pragma unroll
       for (int i = 0; i < 2 * ND; ++i) {
-        adv[i % ND] = mfma_bf16_32x32x16(tr_op(tdO, i), pb[i / ND], adv[i % ND]);
-        adk[i % ND] = mfma_bf16_32x32x16(tr_op(tQ, i), db[i / ND], adk[i % ND]);
+        if (i + 1 < 2 * ND) {
+          ov[(i + 1) & 1] = tr_op(tdO, i + 1);
+          oq[(i + 1) & 1] = tr_op(tQ, i + 1);
+        }
+        adv[i % ND] = mfma_bf16_32x32x16(ov[i & 1], pb[i / ND], adv[i % ND]);
+        adk[i % ND] = mfma_bf16_32x32x16(oq[i & 1], db[i / ND], adk[i % ND]);
       }
     }
   };
