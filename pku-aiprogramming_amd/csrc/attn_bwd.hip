@@ -62,14 +62,15 @@ constexpr int dkdv_bq(int D) { return D == 128 ? 32 : 64; }
 #endif
 constexpr int dkdv_klds(int D) { return D == 128 ? TT_DKDV_KLDS : 0; }
 
-// D_i = sum_d dO[i][d] * O[i][d], one 16-byte chunk per thread; also
-// L2_i = LSE_i * log2(e), the log-sum-exp in the log2 domain the MFMA
-// kernels exponentiate in.
+// ND_i = -D_i = -sum_d dO[i][d] * O[i][d], one 16-byte chunk per thread
+// (stored negated: the dK/dV kernel starts its dP accumulator at -D, so the
+// MFMA yields dP - D directly); also L2_i = LSE_i * log2(e), the log-sum-exp
+// in the log2 domain the MFMA kernels exponentiate in.
 template <typename T, int D>
 __global__ __launch_bounds__(256) void attn_bwd_delta_kernel(const T* __restrict__ O,
                                                              const T* __restrict__ dO,
                                                              const float* __restrict__ LSE,
-                                                             float* __restrict__ Delta, float* __restrict__ L2,
+                                                             float* __restrict__ NDelta, float* __restrict__ L2,
                                                              int64_t rows) {
   constexpr int EPT = 16 / sizeof(T);
   constexpr int TPR = D / EPT;  // threads per row (a power of two <= 32)
@@ -95,7 +96,7 @@ __global__ __launch_bounds__(256) void attn_bwd_delta_kernel(const T* __restrict
 #pragma unroll
   for (int off = TPR / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
   if (col == 0 && row < rows) {
-    Delta[row] = sum;
+    NDelta[row] = -sum;
     L2[row] = LSE[row] * kLog2e;
   }
 }
@@ -104,7 +105,7 @@ __global__ __launch_bounds__(256) void attn_bwd_delta_kernel(const T* __restrict
 template <int D, bool CAUSAL>
 __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_bf16_kernel(
     const u16* __restrict__ Q, const u16* __restrict__ K, const u16* __restrict__ V,
-    const u16* __restrict__ dO, const float* __restrict__ L2, const float* __restrict__ Delta,
+    const u16* __restrict__ dO, const float* __restrict__ L2, const float* __restrict__ NDelta,
     u16* __restrict__ dK, u16* __restrict__ dV, int Lq, int Lk, int BH, int nkt, int group, float sl2,
     float scale) {
   using Tile = SwzTile<D>;
@@ -172,7 +173,7 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_b
       dma.issue(dO + qbase, qb, Lq, sdO + b * TE);
       if (w == 0) {
         load_vec_lds(L2 + lbase + qb, Lq - qb, sL + b * VS);
-        load_vec_lds(Delta + lbase + qb, Lq - qb, sDl + b * VS);
+        load_vec_lds(NDelta + lbase + qb, Lq - qb, sDl + b * VS);
       }
       ++issued;
     }
@@ -182,7 +183,17 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_b
     constexpr bool MASK = decltype(mask_tag)::value;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      f32x16 s = f32x16{}, dp = f32x16{};
+      // dP starts at -D of each query row (register r holds row acc_row(r, g)),
+      // so the accumulator ends as dP - D
+      f32x16 s = f32x16{}, dp;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float4 nd = *reinterpret_cast<const float4*>(&tD[32 * mt + 8 * j + 4 * g]);
+        dp[4 * j] = nd.x;
+        dp[4 * j + 1] = nd.y;
+        dp[4 * j + 2] = nd.z;
+        dp[4 * j + 3] = nd.w;
+      }
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
         const int off = Tile::chunk(32 * mt + r32, 2 * c + g);
@@ -202,9 +213,7 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_b
       for (int j = 0; j < 4; ++j) {
         const int qi = 32 * mt + 8 * j + 4 * g;  // rows acc_row(4j..4j+3, g)
         const float4 lv = *reinterpret_cast<const float4*>(&tL[qi]);
-        const float4 dv = *reinterpret_cast<const float4*>(&tD[qi]);
         const float la[4] = {lv.x, lv.y, lv.z, lv.w};
-        const float da[4] = {dv.x, dv.y, dv.z, dv.w};
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
           const int r = 4 * j + u;
@@ -214,7 +223,7 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_b
             if (q >= Lq || (CAUSAL && key > q)) p = 0.f;
           }
           pb[r >> 3][r & 7] = (__bf16)p;
-          db[r >> 3][r & 7] = (__bf16)(p * (dp[r] - da[u]));
+          db[r >> 3][r & 7] = (__bf16)(p * dp[r]);
         }
       }
       // dV^T += dO^T P and dK^T += Q^T dS over the 32 queries of this half:
@@ -293,7 +302,7 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_b
 template <int D, bool CAUSAL>
 __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dq_bf16_kernel(
     const u16* __restrict__ Q, const u16* __restrict__ K, const u16* __restrict__ V,
-    const u16* __restrict__ dO, const float* __restrict__ L2, const float* __restrict__ Delta,
+    const u16* __restrict__ dO, const float* __restrict__ L2, const float* __restrict__ NDelta,
     u16* __restrict__ dQ, int Lq, int Lk, int BH, int nqt, int group, float sl2, float scale) {
   using Tile = SwzTile<D>;
   constexpr int NW = bwd_nw(D), BM = 32 * NW, BN = DQ_BN, S = kBwdStages;
@@ -325,7 +334,7 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dq_bf1
   }
   // padding query rows (qrow >= Lq): P = 2^(s - inf) = 0
   const float lse2 = qrow < Lq ? L2[(int64_t)bh * Lq + qrow] : INFINITY;
-  const float dl = qrow < Lq ? Delta[(int64_t)bh * Lq + qrow] : 0.f;
+  const float ndl = qrow < Lq ? NDelta[(int64_t)bh * Lq + qrow] : 0.f;
   f32x16 adq[ND];
 #pragma unroll
   for (int dt = 0; dt < ND; ++dt) adq[dt] = f32x16{};
@@ -384,7 +393,7 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dq_bf1
           const int kk = kb + 32 * t + acc_row(r, g);
           if (kk >= Lk || (CAUSAL && kk > qrow)) p = 0.f;
         }
-        db[r >> 3][r & 7] = (__bf16)(p * (dp[r] - dl));
+        db[r >> 3][r & 7] = (__bf16)(p * (dp[r] + ndl));
       }
 #pragma unroll
       for (int i = 0; i < 2 * ND; ++i) {
@@ -430,7 +439,7 @@ template <typename T, int D, bool CAUSAL>
 static int launch_bwd(const T* q, const T* k, const T* v, const T* o, const float* lse, const T* dout,
                       T* dq, T* dk, T* dv, int64_t BH, int64_t Lq, int64_t Lk, float scale, hipStream_t st) {
   constexpr bool BF = sizeof(T) == 2;
-  // workspace: D (row sums of dO o O) and LSE * log2(e), fp32 [B*H*Lq] each
+  // workspace: -D (negated row sums of dO o O) and LSE * log2(e), fp32 [B*H*Lq] each
   float* delta = nullptr;
   int rc = workspace(0, (size_t)(2 * BH * Lq) * sizeof(float), (void**)&delta);
   if (rc) return rc;

@@ -16,7 +16,7 @@ constexpr int BWD_F32_KN = 64;   // keys per LDS step of the dQ kernel
 template <int D, bool CAUSAL>
 __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_f32_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
-    const float* __restrict__ dO, const float* __restrict__ LSE, const float* __restrict__ Delta,
+    const float* __restrict__ dO, const float* __restrict__ LSE, const float* __restrict__ NDelta,
     float* __restrict__ dK, float* __restrict__ dV, int Lq, int Lk, int BH, int nkt, int group,
     float sl2, float scale) {
   constexpr int BN = BWD_F32_BN, BQ = BWD_F32_BQ;
@@ -64,7 +64,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_f32_kernel(
     if (tid < BQ) {
       const bool in = qb + tid < Lq;
       lreg = in ? LSE[lbase + qb + tid] * kLog2e : INFINITY;
-      dreg = in ? Delta[lbase + qb + tid] : 0.f;
+      dreg = in ? NDelta[lbase + qb + tid] : 0.f;
     }
   };
   auto sstore = [&]() {
@@ -107,7 +107,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_f32_kernel(
         float p = fast_exp2(fmaf(s[r], sl2, -sL[qi]));
         if (need_mask && key > qb + qi) p = 0.f;
         pr[r] = p;
-        dsr[r] = p * (dp[r] - sDl[qi]);
+        dsr[r] = p * (dp[r] + sDl[qi]);
       }
 #pragma unroll
       for (int dt = 0; dt < ND; ++dt)
@@ -140,7 +140,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_f32_kernel(
 template <int D, bool CAUSAL>
 __global__ __launch_bounds__(256, 1) void attn_bwd_dq_f32_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
-    const float* __restrict__ dO, const float* __restrict__ LSE, const float* __restrict__ Delta,
+    const float* __restrict__ dO, const float* __restrict__ LSE, const float* __restrict__ NDelta,
     float* __restrict__ dQ, int Lq, int Lk, int BH, int nqt, int group, float sl2, float scale) {
   constexpr int BM = BWD_F32_BM, BN = BWD_F32_KN;
   constexpr int P = D + 1;
@@ -168,7 +168,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_f32_kernel(
     }
   }
   const float lse2 = qrow < Lq ? LSE[(int64_t)bh * Lq + qrow] * kLog2e : INFINITY;
-  const float dl = qrow < Lq ? Delta[(int64_t)bh * Lq + qrow] : 0.f;
+  const float ndl = qrow < Lq ? NDelta[(int64_t)bh * Lq + qrow] : 0.f;
   f32x16 adq[ND];
 #pragma unroll
   for (int dt = 0; dt < ND; ++dt) adq[dt] = f32x16{};
@@ -220,7 +220,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_f32_kernel(
           const int kk = kb + 32 * t + acc_row(r, g);
           if (kk >= Lk || (CAUSAL && kk > qrow)) p = 0.f;
         }
-        dsr[r] = p * (dp[r] - dl);
+        dsr[r] = p * (dp[r] + ndl);
       }
 #pragma unroll
       for (int dt = 0; dt < ND; ++dt)
