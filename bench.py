@@ -48,11 +48,11 @@ C4 = dict(B=64, H=32, Lkv=8192, d=128)
 # write x1.000); the commands and raw counters are in
 # profiles/hbm_traffic_c5_c4.md.  Re-measured whenever a kernel changes.
 MEASURED_TRAFFIC_MIB = {
-    "attn_fwd": 648.8,
-    "attn_bwd_delta": 258.0,
-    "attn_bwd_dkdv": 772.3,
-    "attn_bwd_dq": 644.2,
-    "attn_decode_split": 8217.6,
+    "attn_fwd": 574.7,
+    "attn_bwd_delta": 264.0,
+    "attn_bwd_dkdv": 862.1,
+    "attn_bwd_dq": 768.1,
+    "attn_decode_split": 8217.7,
 }
 
 
