@@ -62,6 +62,43 @@ __device__ __forceinline__ constexpr int perm16(int j) {
 
 __device__ __forceinline__ float wave_xor32(float x) { return __shfl_xor(x, 32, 64); }
 
+// Reductions over lanes l and l ^ 32 in two VALU ops, with no LDS round
+// trip: v_permlane32_swap of x with a copy of itself returns r[0] = lanes
+// 0..31 of x in both halves and r[1] = lanes 32..63 in both halves (checked
+// on the MI355X).  Both halves compute the same expression, so they agree
+// bit for bit.
+__device__ __forceinline__ float max_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+__device__ __forceinline__ float fmax3(float a, float b, float c) { return fmaxf(fmaxf(a, b), c); }
+
+// acc + the two bf16 halves of element e (a bf16 pair) of v, by one
+// v_dot2_f32_bf16 against (1, 1).
+__device__ __forceinline__ float sum_bf16x2(const bf16x8& v, int e, float acc) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  const bf16x2 pair = {v[2 * e], v[2 * e + 1]};
+  const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+  return __builtin_amdgcn_fdot2_f32_bf16(pair, one, acc, false);
+}
+
+// Keep an MFMA accumulator in AGPRs: an empty asm that takes the value in
+// AGPRs.  Kernels built with VGPR-form MFMAs (-amdgpu-mfma-vgpr-form) then
+// give the accumulating MFMA an AGPR destination and source C, leaving the
+// VGPRs to the operands and the score tiles the VALU works on.  It emits no
+// instruction, so the compiler's MFMA hazard handling is unaffected.
+__device__ __forceinline__ void pin_agpr(f32x16& acc) { asm volatile("" : "+a"(acc)); }
+
+// Instruction classes of __builtin_amdgcn_sched_group_barrier.
+constexpr int kSchedMFMA = 0x008;
+constexpr int kSchedVALU = 0x002 | 0x400;  // VALU incl. transcendental
+constexpr int kSchedDSRead = 0x100;
+
 // Exact power-of-two exponent: v_exp_f32 computes 2^x.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
@@ -155,24 +192,31 @@ __device__ __forceinline__ void glds4(const void* sbase, uint32_t voff, uint32_t
 // Load instruction i of wave w fills the 64 consecutive 16-byte LDS slots
 // starting at slot 64 (i NW + w); each lane fetches the global chunk that
 // belongs in its slot.  One instruction covers 64 / kCPR rows, so step i
-// moves NW * 64 / kCPR rows on; every swizzle has a period dividing 16
-// rows, so when that step is a multiple of 16 the lane's chunk column is the
-// same for every i and the byte offset is voff + 1024 NW i, with voff
-// computed once.
+// moves kStep = NW * 64 / kCPR rows on.  Every swizzle has a period
+// dividing 16 rows, so the lane's chunk column repeats every kPh = 16 /
+// gcd(kStep, 16) instructions: instruction i reads at byte offset
+// voff[i % kPh] + 2 D kStep (i - i % kPh), with the kPh offsets computed
+// once.
 template <int D, int ROWS, int NW>
 struct TileDma {
   static constexpr int kCPR = D / 8;
   static_assert(ROWS * kCPR % (64 * NW) == 0, "tile must split evenly over the waves");
-  static_assert((NW * 64 / kCPR) % 16 == 0, "row step must keep the swizzle phase");
+  static constexpr int kStep = NW * 64 / kCPR;  // rows per load instruction of the workgroup
+  static_assert(kStep % 16 == 0 || 16 % kStep == 0, "row step must divide or be a multiple of 16");
+  static constexpr int kPh = kStep % 16 == 0 ? 1 : 16 / kStep;
   static constexpr int kLoads = ROWS * kCPR / (64 * NW);  // load instructions per wave per tile
-  uint32_t voff;  // this lane's byte offset for instruction 0, from the tile's first row
+  static_assert(kLoads % kPh == 0 || kLoads < kPh, "loads must cover whole swizzle periods");
+  uint32_t voff[kPh];  // this lane's byte offsets for instructions 0..kPh-1, from the tile's first row
   int w;
 
   __device__ __forceinline__ void init() {
     w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int p = w * 64 + (threadIdx.x & 63);
-    const int row = p / kCPR, ch = (p % kCPR) ^ SwzTile<D>::sw(row);
-    voff = 2u * (uint32_t)(row * D + 8 * ch);
+#pragma unroll
+    for (int ph = 0; ph < kPh; ++ph) {
+      const int row = p / kCPR + ph * kStep, ch = (p % kCPR) ^ SwzTile<D>::sw(row);
+      voff[ph] = 2u * (uint32_t)(row * D + 8 * ch);
+    }
   }
   // Issue the loads of rows [row0, row0 + ROWS) of `src` into the tile at
   // `dst`.  Requires 0 <= row0 < rmax; rows >= rmax read row rmax - 1 instead
@@ -182,13 +226,16 @@ struct TileDma {
     const uint32_t lds = lds_addr(dst) + 1024u * (uint32_t)w;
     if (row0 + ROWS <= rmax) {
 #pragma unroll
-      for (int i = 0; i < kLoads; ++i) glds16(base + 512 * NW * i, voff, lds + 1024u * NW * i);
+      for (int i = 0; i < kLoads; ++i)
+        glds16(base + (int64_t)D * kStep * (i - i % kPh), voff[i % kPh], lds + 1024u * NW * i);
     } else {
       const int p0 = w * 64 + (threadIdx.x & 63);
-      const int r0 = p0 / kCPR, ch = (p0 % kCPR) ^ SwzTile<D>::sw(r0);
+      const int r0 = p0 / kCPR;
 #pragma unroll
       for (int i = 0; i < kLoads; ++i) {
-        const int row = min(r0 + i * (NW * 64 / kCPR), rmax - 1 - row0);
+        // the slot's chunk column follows the swizzle of its own (unclamped) row
+        const int ch = (p0 % kCPR) ^ SwzTile<D>::sw(r0 + i * kStep);
+        const int row = min(r0 + i * kStep, rmax - 1 - row0);
         glds16(base, 2u * (uint32_t)(row * D + 8 * ch), lds + 1024u * NW * i);
       }
     }

@@ -230,6 +230,300 @@ __global__ __launch_bounds__(64 * fwd_nw(D), 8 / fwd_nw(D)) void attn_fwd_bf16_k
   }
 }
 
+// ---------------------------------------------------------------------------
+// Software-pipelined bf16 forward (D = 64, 128).
+//
+// Workgroup = NW waves x 32 queries (lane l: query wq0 + l % 32), two
+// workgroups per CU (two waves per SIMD).  Key tiles of 64; iteration j:
+//   phase 1  MFMA  S_{j+1} = K_{j+1} Q^T
+//            VALU  P_j = 2^(s S_j - m), P_j -> bf16
+//   phase 2  MFMA  O^T += V_j^T P_j^T
+//            VALU  l += sum P_j; running max from S_{j+1} (lazy, branch-free)
+// so the softmax of one tile runs on the VALU while the matrix cores compute
+// the next tile's scores (__builtin_amdgcn_sched_group_barrier interleaves
+// the two instruction streams), and the other wave of the SIMD fills what is
+// left.  The K ring runs one tile ahead of the V ring: pair n = (K_{n+1},
+// V_n) is waited for at barrier n (before iteration n) and pair n + 1 is
+// issued right after it into the buffers of K_n and V_{n-1}, which
+// iterations up to n - 1 have finished with.
+constexpr int FWDP_NW = 4;  // waves per workgroup
+
+template <int D, bool CAUSAL, int NW>
+__global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fwd_bf16_pipe_kernel(
+    const u16* __restrict__ Q, const u16* __restrict__ K, const u16* __restrict__ V,
+    u16* __restrict__ O, float* __restrict__ LSE, int Lq, int Lk, int BH, int nqt, int group,
+    float sl2) {
+  using Tile = SwzTile<D>;
+  constexpr int BM = 32 * NW, BN = 64;
+  constexpr int NC = D / 16, ND = D / 32;
+  constexpr int TE = Tile::kElems(BN);
+  using Dma = TileDma<D, BN, NW>;
+  __shared__ __align__(16) u16 sK[2 * TE];
+  __shared__ __align__(16) u16 sV[2 * TE];
+
+  // the wave index is wave-uniform: loop bounds derived from it stay scalar
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l = threadIdx.x & 63, g = l >> 5, r32 = l & 31;
+  int qt, bh;
+  map_tile(blockIdx.x, nqt, BH, group, qt, bh, CAUSAL);
+  const int q0 = qt * BM, wq0 = q0 + 32 * w, qrow = wq0 + r32;
+  const int64_t qbase = (int64_t)bh * Lq * D;
+  const int64_t kbase = (int64_t)bh * Lk * D;
+
+  bf16x8 qf[NC];
+  {
+    const int qr = min(qrow, Lq - 1);  // padding rows read a valid row; never written back
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+      qf[c] = __builtin_bit_cast(bf16x8, ldg16(Q + qbase + (int64_t)qr * D + 16 * c + 8 * g));
+  }
+
+  const int kend = CAUSAL ? min(Lk, q0 + BM) : Lk;  // >= 1: Lk >= 1, and q0 < Lq = Lk when causal
+  const int ntiles = (kend + BN - 1) / BN;
+  // Last tile this wave computes: its diagonal tile (causal) or the last
+  // tile.  Every earlier tile lies inside Lk and before every query of the
+  // wave, so only the last one can need a mask.
+  const int last = CAUSAL ? min(wq0 / BN, ntiles - 1) : ntiles - 1;
+  const bool mask_last = CAUSAL || (Lk % BN) != 0;
+
+  // Per-lane LDS element offsets.  K operand of chunk c: key row r32 (+32
+  // for the second key half), 16-byte chunk 2c + g.  V^T operand of d-tile
+  // dt: transpose reads of rows vrow and vrow + 8 (+16 per key chunk),
+  // column 32 dt + vcol.  Rows 16 apart share a swizzle, so the key-half and
+  // key-chunk steps are constant offsets.
+  int kidx[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) kidx[c] = Tile::chunk(r32, 2 * c + g);
+  const int t16 = l & 15;
+  const int vcol = 16 * ((l >> 4) & 1) + 4 * (t16 & 3);
+  const int vrow = 4 * g + (t16 >> 2);
+  int vidx[2][ND];
+#pragma unroll
+  for (int dt = 0; dt < ND; ++dt) {
+    vidx[0][dt] = Tile::at4(vrow, 32 * dt + vcol);
+    vidx[1][dt] = Tile::at4(vrow + 8, 32 * dt + vcol);
+  }
+
+  f32x16 o[ND];
+#pragma unroll
+  for (int dt = 0; dt < ND; ++dt) o[dt] = f32x16{};
+  f32x16 sa[2], sb[2];  // S^T of two consecutive tiles (key half t = 0, 1)
+  bf16x8 pb[4];         // P^T operands (16-key chunk)
+  float m, lsum = 0.f, alpha = 1.f;
+  bool rescale = false;
+
+  auto qk = [&](const u16* tK, f32x16(&s)[2]) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const bf16x8 k0 = *reinterpret_cast<const bf16x8*>(&tK[kidx[c]]);
+      const bf16x8 k1 = *reinterpret_cast<const bf16x8*>(&tK[kidx[c] + 32 * D]);
+      s[0] = mfma_bf16_32x32x16(k0, qf[c], c == 0 ? f32x16{} : s[0]);
+      s[1] = mfma_bf16_32x32x16(k1, qf[c], c == 0 ? f32x16{} : s[1]);
+    }
+  };
+  auto mask_tile = [&](f32x16(&s)[2], int kb) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = kb + 32 * t + acc_row(r, g);
+        if (key >= Lk || (CAUSAL && key > qrow)) s[t][r] = -INFINITY;
+      }
+  };
+  // Running max per query, in the log2 domain.  It moves only when some
+  // lane's tile max exceeds it by more than 8, so p = 2^(x - m) <= 256 and
+  // the O rescale is skipped on most tiles; the result is exact either way
+  // (numerator and denominator share m).  Returns whether O must be
+  // rescaled by alpha before the next PV.
+  auto row_max = [&](const f32x16(&s)[2], bool first) {
+    // four independent v_max3 chains over the 32 scores of this lane
+    float x[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      x[c] = fmaxf(s[c >> 1][8 * (c & 1)], s[c >> 1][8 * (c & 1) + 1]);
+#pragma unroll
+      for (int r = 2; r < 8; r += 2) x[c] = fmax3(x[c], s[c >> 1][8 * (c & 1) + r], s[c >> 1][8 * (c & 1) + r + 1]);
+    }
+    const float mx = max_xor32(fmaxf(fmax3(x[0], x[1], x[2]), x[3])) * sl2;
+    if (first) {
+      m = mx;
+      return false;
+    }
+    const bool need = wave_any(mx > m + 8.f);
+    const float mn = need ? fmaxf(m, mx) : m;
+    alpha = fast_exp2(m - mn);  // exactly 1 when m is unchanged; 0 when m was -inf
+    m = mn;
+    lsum *= alpha;
+    return need;
+  };
+  // p = 2^(s sl2 - m) in place, and the bf16 P^T operands
+  auto exp_cvt = [&](f32x16(&s)[2]) {
+    const float mb = m == -INFINITY ? 0.f : m;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[t][r] = fast_exp2(fmaf(s[t][r], sl2, -mb));
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) pb[kc][e] = (__bf16)s[kc >> 1][8 * (kc & 1) + e];
+  };
+  // Row sum of the bf16-rounded P, the weights the PV MFMAs apply:
+  // v_dot2_f32_bf16 against (1, 1) adds two of them per instruction.
+  auto add_sum = [&]() {
+    float ps[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ps[e] = sum_bf16x2(pb[kc], e, ps[e]);
+    lsum += (ps[0] + ps[1]) + (ps[2] + ps[3]);
+  };
+  auto pv = [&](const u16* tV) {
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc)
+#pragma unroll
+      for (int dt = 0; dt < ND; ++dt) {
+        const bf16x8 v = lds_read_tr16x2(&tV[vidx[0][dt] + 16 * D * kc], &tV[vidx[1][dt] + 16 * D * kc]);
+        o[dt] = mfma_bf16_32x32x16(v, pb[kc], o[dt]);
+      }
+  };
+  auto rescale_o = [&]() {
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt) o[dt] *= alpha;
+  };
+
+  Dma dma;
+  dma.init();
+  auto issue_k = [&](int n) {
+    if (n < ntiles) dma.issue(K + kbase, BN * n, Lk, sK + (n & 1) * TE);
+  };
+  auto issue_v = [&](int n) {
+    if (n < ntiles) dma.issue(V + kbase, BN * n, Lk, sV + (n & 1) * TE);
+  };
+  auto step = [&](int n) {
+    wait_vmem_le<0>();
+    __syncthreads();
+    issue_k(n + 2);
+    issue_v(n + 1);
+  };
+
+  // Interleave patterns: one MFMA at a time with the VALU work that fits
+  // beside it.
+  constexpr int kP1Mfma = 2 * NC, kP1Valu = 32 * 2 + 16 + 2;
+  constexpr int kP1VPer = (kP1Valu + kP1Mfma - 1) / kP1Mfma;
+  constexpr int kP2Mfma = 4 * ND, kP2Valu = 16 + 20 + 12;
+  constexpr int kP2VPer = (kP2Valu + kP2Mfma - 1) / kP2Mfma;
+  auto sched_phase1 = [&]() {
+    __builtin_amdgcn_sched_group_barrier(kSchedDSRead, 2, 0);
+    __builtin_amdgcn_sched_group_barrier(kSchedVALU, 4, 0);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      if (c + 1 < NC) __builtin_amdgcn_sched_group_barrier(kSchedDSRead, 2, 0);
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        __builtin_amdgcn_sched_group_barrier(kSchedMFMA, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedVALU, kP1VPer, 0);
+      }
+    }
+  };
+  auto sched_phase2 = [&]() {
+    __builtin_amdgcn_sched_group_barrier(kSchedDSRead, 2, 0);
+#pragma unroll
+    for (int i = 0; i < 4 * ND; ++i) {
+      if (i + 1 < 4 * ND) __builtin_amdgcn_sched_group_barrier(kSchedDSRead, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedMFMA, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedVALU, kP2VPer, 0);
+    }
+  };
+
+  // Iteration j: barrier j, S_{j+1} from K_{j+1} into `nx` while the
+  // softmax of `cur` (tile j) runs, then PV of tile j and the max of tile j + 1.
+  // PAR = j & 1 when known at compile time (the buffers' LDS offsets then
+  // fold into the read instructions), -1 otherwise.
+  auto body = [&](int j, f32x16(&cur)[2], f32x16(&nx)[2], auto mask_tag, auto par_tag) {
+    constexpr bool MASK = decltype(mask_tag)::value;
+    constexpr int PAR = decltype(par_tag)::value;
+    const int kbuf = PAR < 0 ? ((j + 1) & 1) : 1 - PAR, vbuf = PAR < 0 ? (j & 1) : PAR;
+    step(j);
+    // the rare O rescale goes first, so that both phases form one basic
+    // block for the scheduler
+    if (rescale) rescale_o();
+    qk(sK + kbuf * TE, nx);
+    exp_cvt(cur);
+    sched_phase1();
+    pv(sV + vbuf * TE);
+    add_sum();
+    if constexpr (MASK) mask_tile(nx, BN * (j + 1));
+    rescale = row_max(nx, false);
+    sched_phase2();
+  };
+
+  // Prologue: K_0, then pair 0 (K_1, V_0); S_0 once K_0 has landed.
+  issue_k(0);
+  issue_k(1);
+  issue_v(0);
+  if (ntiles > 1)
+    wait_vmem_le<2 * Dma::kLoads>();
+  else
+    wait_vmem_le<Dma::kLoads>();
+  __syncthreads();
+  qk(sK, sa);
+  if (last == 0 && mask_last) mask_tile(sa, 0);
+  row_max(sa, true);
+
+  // Unmasked iterations 0 .. last - 2 in pairs (the score tiles swap roles),
+  // then iteration last - 1, whose next tile is the wave's last one.
+  using Even = std::integral_constant<int, 0>;
+  using Odd = std::integral_constant<int, 1>;
+  using Any = std::integral_constant<int, -1>;
+  int j = 0;
+  for (; j + 1 < last - 1; j += 2) {
+    body(j, sa, sb, std::false_type{}, Even{});
+    body(j + 1, sb, sa, std::false_type{}, Odd{});
+  }
+  if (j < last - 1) {
+    body(j, sa, sb, std::false_type{}, Any{});
+    sa[0] = sb[0];
+    sa[1] = sb[1];
+    ++j;
+  }
+  if (last >= 1) {
+    if (mask_last)
+      body(j, sa, sb, std::true_type{}, Any{});
+    else
+      body(j, sa, sb, std::false_type{}, Any{});
+    sa[0] = sb[0];
+    sa[1] = sb[1];
+  }
+  // Last tile of this wave: softmax and PV only.
+  step(last);
+  if (rescale) rescale_o();
+  exp_cvt(sa);
+  pv(sV + (last & 1) * TE);
+  add_sum();
+  // Later tiles belong to other waves of the workgroup: take part in their
+  // barriers and loads.
+  for (int n = last + 1; n < ntiles; ++n) step(n);
+  wait_vmem_le<0>();  // nothing may be in flight into LDS when the workgroup exits
+
+  const float ls = sum_xor32(lsum);
+  if (qrow < Lq) {
+    const float inv = ls > 0.f ? 1.f / ls : 0.f;
+    u16* orow = O + qbase + (int64_t)qrow * D;
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; r += 4) {
+        const int d0 = 32 * dt + acc_row(r, g);
+        uint2 v;
+        v.x = pack_bf16x2(o[dt][r] * inv, o[dt][r + 1] * inv);
+        v.y = pack_bf16x2(o[dt][r + 2] * inv, o[dt][r + 3] * inv);
+        *reinterpret_cast<uint2*>(orow + d0) = v;
+      }
+    if (g == 0 && LSE) LSE[(int64_t)bh * Lq + qrow] = (m + __log2f(ls)) * kLn2;
+  }
+}
+
 template <int D, bool CAUSAL>
 __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void attn_fwd_f32_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
@@ -360,14 +654,14 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void attn_fwd_f32_kernel(
 }
 
 template <typename T, typename KernelPtr>
-static int launch_fwd(KernelPtr kern, int bm, int threads, const T* q, const T* k, const T* v, T* o,
-                      float* lse, int64_t BH, int64_t Lq, int64_t Lk, float scale, hipStream_t s) {
+static int launch_fwd(KernelPtr kern, int bm, int threads, int wg_per_cu, const T* q, const T* k, const T* v,
+                      T* o, float* lse, int64_t BH, int64_t Lq, int64_t Lk, float scale, hipStream_t s) {
   const int64_t nqt = (Lq + bm - 1) / bm;
   const int64_t nblk = nqt * BH;
   if (nblk > 0x7fffffff) return fail(TT_ERR_ARG, "attention forward: grid too large");
   // heads in flight per XCD: enough tiles for the resident workgroups of its
-  // 32 CUs (8 waves per CU: 2 per SIMD)
-  const int group = pick_group(BH, nqt, 32 * (512 / threads));
+  // 32 CUs
+  const int group = pick_group(BH, nqt, 32 * wg_per_cu);
   hipLaunchKernelGGL(kern, dim3((unsigned)nblk), dim3(threads), 0, s, q, k, v, o, lse, (int)Lq, (int)Lk,
                      (int)BH, (int)nqt, group, scale * kLog2e);
   TT_LAUNCHED("attention forward launch", s);
@@ -377,14 +671,22 @@ static int launch_fwd(KernelPtr kern, int bm, int threads, const T* q, const T* 
 template <int D, bool CAUSAL>
 static int fwd_bf16(const u16* q, const u16* k, const u16* v, u16* o, float* lse, int64_t BH, int64_t Lq,
                     int64_t Lk, float scale, hipStream_t st) {
-  constexpr int NW = fwd_nw(D);
-  return launch_fwd(attn_fwd_bf16_kernel<D, CAUSAL>, 32 * NW, 64 * NW, q, k, v, o, lse, BH, Lq, Lk, scale, st);
+  if constexpr (D >= 64) {
+    // two waves per SIMD: two FWDP_NW-wave workgroups per CU
+    constexpr int NW = FWDP_NW;
+    return launch_fwd(attn_fwd_bf16_pipe_kernel<D, CAUSAL, NW>, 32 * NW, 64 * NW, 8 / NW, q, k, v, o, lse, BH, Lq,
+                      Lk, scale, st);
+  } else {
+    constexpr int NW = fwd_nw(D);
+    return launch_fwd(attn_fwd_bf16_kernel<D, CAUSAL>, 32 * NW, 64 * NW, 8 / NW, q, k, v, o, lse, BH, Lq, Lk,
+                      scale, st);
+  }
 }
 
 template <int D, bool CAUSAL>
 static int fwd_f32(const float* q, const float* k, const float* v, float* o, float* lse, int64_t BH, int64_t Lq,
                    int64_t Lk, float scale, hipStream_t st) {
-  return launch_fwd(attn_fwd_f32_kernel<D, CAUSAL>, FWD_F32_BM, 256, q, k, v, o, lse, BH, Lq, Lk, scale, st);
+  return launch_fwd(attn_fwd_f32_kernel<D, CAUSAL>, FWD_F32_BM, 256, 2, q, k, v, o, lse, BH, Lq, Lk, scale, st);
 }
 
 }  // namespace tt

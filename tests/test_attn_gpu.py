@@ -175,7 +175,11 @@ def test_c4_bf16_decode(capi):
     capi.lib().sync()
     od, ld = o.download(), lse.download()
     _check("decode vs forward kernel O", od, o2.download(), TOL["bf16"])
-    _check("decode vs forward kernel LSE", ld, lse2.download()[..., 0], 1e-5)
+    # The bf16 forward normalises by the sum of the bf16-rounded weights its
+    # PV MFMAs apply (relative error <= 2^-9 against an fp32 sum); the decode
+    # kernel sums in fp32.  The two LSEs agree to that bound; both are checked
+    # against the float64 oracle below.
+    _check("decode vs forward kernel LSE", ld, lse2.download()[..., 0], 2.0 ** -9)
     qh = q.download()
     # sampled heads: copy their K/V rows back (bh-contiguous slabs)
     for (bb, hh) in [(0, 0), (33, 17), (63, 31)]:
