@@ -218,6 +218,15 @@ struct TileDma {
       voff[ph] = 2u * (uint32_t)(row * D + 8 * ch);
     }
   }
+  // Issue load instruction i (0 <= i < kLoads) of the tile of rows
+  // [row0, row0 + ROWS) of `src`, which must lie inside the matrix.  Kernels
+  // spread a tile's instructions over their compute: issued back to back
+  // right after a barrier, the loads of every wave queue at the CU's texture
+  // address unit and each wave stalls until its own are accepted.
+  __device__ __forceinline__ void issue_one(const u16* src, int row0, const u16* dst, int i) const {
+    glds16(src + (int64_t)row0 * D + (int64_t)D * kStep * (i - i % kPh), voff[i % kPh],
+           lds_addr(dst) + 1024u * (uint32_t)(w + NW * i));
+  }
   // Issue the loads of rows [row0, row0 + ROWS) of `src` into the tile at
   // `dst`.  Requires 0 <= row0 < rmax; rows >= rmax read row rmax - 1 instead
   // (callers mask them).  Completion: a vmcnt wait, then a barrier.

@@ -246,7 +246,19 @@ __global__ __launch_bounds__(64 * fwd_nw(D), 8 / fwd_nw(D)) void attn_fwd_bf16_k
 // V_n) is waited for at barrier n (before iteration n) and pair n + 1 is
 // issued right after it into the buffers of K_n and V_{n-1}, which
 // iterations up to n - 1 have finished with.
-constexpr int FWDP_NW = 4;  // waves per workgroup
+#ifndef TT_FWDP_NW
+#define TT_FWDP_NW 4
+#endif
+constexpr int FWDP_NW = TT_FWDP_NW;  // waves per workgroup
+#ifndef TT_FWDP_SCHED
+#define TT_FWDP_SCHED 1  // interleave MFMA / VALU / LDS reads by sched_group_barrier
+#endif
+#ifndef TT_FWDP_KAHEAD
+#define TT_FWDP_KAHEAD 2  // K chunks read ahead of their MFMAs
+#endif
+#ifndef TT_FWDP_VAHEAD
+#define TT_FWDP_VAHEAD 3  // V^T operands read ahead of their MFMAs
+#endif
 
 template <int D, bool CAUSAL, int NW>
 __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fwd_bf16_pipe_kernel(
@@ -312,15 +324,21 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fwd_bf16_pipe_kernel(
   float m, lsum = 0.f, alpha = 1.f;
   bool rescale = false;
 
-  auto qk = [&](const u16* tK, f32x16(&s)[2]) {
+  // `load(c)` runs after the MFMAs of chunk c; the pipelined loop issues
+  // one tile-load instruction of the next pair there (K, then V).
+  constexpr int kLoads = Dma::kLoads;
+  static_assert(2 * kLoads <= NC, "a K and a V tile load per chunk of the contraction");
+  auto qk = [&](const u16* tK, f32x16(&s)[2], auto load) {
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       const bf16x8 k0 = *reinterpret_cast<const bf16x8*>(&tK[kidx[c]]);
       const bf16x8 k1 = *reinterpret_cast<const bf16x8*>(&tK[kidx[c] + 32 * D]);
       s[0] = mfma_bf16_32x32x16(k0, qf[c], c == 0 ? f32x16{} : s[0]);
       s[1] = mfma_bf16_32x32x16(k1, qf[c], c == 0 ? f32x16{} : s[1]);
+      load(c);
     }
   };
+  auto no_load = [](int) {};
   auto mask_tile = [&](f32x16(&s)[2], int kb) {
 #pragma unroll
     for (int t = 0; t < 2; ++t)
@@ -408,47 +426,74 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fwd_bf16_pipe_kernel(
   };
 
   // Interleave patterns: one MFMA at a time with the VALU work that fits
-  // beside it.
+  // beside it; LDS operand reads run TT_FWDP_KAHEAD K chunks / TT_FWDP_VAHEAD
+  // V^T operands ahead of the MFMAs that consume them, and the first V^T
+  // operands are fetched at the end of phase 1.
   constexpr int kP1Mfma = 2 * NC, kP1Valu = 32 * 2 + 16 + 2;
   constexpr int kP1VPer = (kP1Valu + kP1Mfma - 1) / kP1Mfma;
   constexpr int kP2Mfma = 4 * ND, kP2Valu = 16 + 20 + 12;
   constexpr int kP2VPer = (kP2Valu + kP2Mfma - 1) / kP2Mfma;
+  constexpr int KA = TT_FWDP_KAHEAD < NC ? TT_FWDP_KAHEAD : NC;
+  constexpr int VA = TT_FWDP_VAHEAD < 4 * ND ? TT_FWDP_VAHEAD : 4 * ND;
   auto sched_phase1 = [&]() {
-    __builtin_amdgcn_sched_group_barrier(kSchedDSRead, 2, 0);
-    __builtin_amdgcn_sched_group_barrier(kSchedVALU, 4, 0);
+    if constexpr (TT_FWDP_SCHED) {
+      __builtin_amdgcn_sched_group_barrier(kSchedDSRead, 2 * KA, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedVALU, 4, 0);
 #pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      if (c + 1 < NC) __builtin_amdgcn_sched_group_barrier(kSchedDSRead, 2, 0);
+      for (int c = 0; c < NC; ++c) {
+        if (c + KA < NC) __builtin_amdgcn_sched_group_barrier(kSchedDSRead, 2, 0);
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        __builtin_amdgcn_sched_group_barrier(kSchedMFMA, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(kSchedVALU, kP1VPer, 0);
+        for (int i = 0; i < 2; ++i) {
+          __builtin_amdgcn_sched_group_barrier(kSchedMFMA, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(kSchedVALU, kP1VPer, 0);
+        }
       }
+      __builtin_amdgcn_sched_group_barrier(kSchedDSRead, 2 * VA, 0);
     }
   };
   auto sched_phase2 = [&]() {
-    __builtin_amdgcn_sched_group_barrier(kSchedDSRead, 2, 0);
+    if constexpr (TT_FWDP_SCHED) {
 #pragma unroll
-    for (int i = 0; i < 4 * ND; ++i) {
-      if (i + 1 < 4 * ND) __builtin_amdgcn_sched_group_barrier(kSchedDSRead, 2, 0);
-      __builtin_amdgcn_sched_group_barrier(kSchedMFMA, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(kSchedVALU, kP2VPer, 0);
+      for (int i = 0; i < 4 * ND; ++i) {
+        if (i + VA < 4 * ND) __builtin_amdgcn_sched_group_barrier(kSchedDSRead, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedMFMA, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedVALU, kP2VPer, 0);
+      }
     }
   };
 
   // Iteration j: barrier j, S_{j+1} from K_{j+1} into `nx` while the
   // softmax of `cur` (tile j) runs, then PV of tile j and the max of tile j + 1.
   // PAR = j & 1 when known at compile time (the buffers' LDS offsets then
-  // fold into the read instructions), -1 otherwise.
-  auto body = [&](int j, f32x16(&cur)[2], f32x16(&nx)[2], auto mask_tag, auto par_tag) {
+  // fold into the read instructions), -1 otherwise.  SPREAD: the pair this
+  // iteration loads (K_{j+2}, V_{j+1}) exists and lies inside Lk, and its
+  // load instructions are spread over the phase-1 MFMAs (early enough to land
+  // by the next barrier) instead of issued back to back after the barrier.
+  auto body = [&](int j, f32x16(&cur)[2], f32x16(&nx)[2], auto mask_tag, auto par_tag, auto spread_tag) {
     constexpr bool MASK = decltype(mask_tag)::value;
     constexpr int PAR = decltype(par_tag)::value;
+    constexpr bool SPREAD = decltype(spread_tag)::value;
+    static_assert(!SPREAD || PAR >= 0, "spread loads need the ring parity");
     const int kbuf = PAR < 0 ? ((j + 1) & 1) : 1 - PAR, vbuf = PAR < 0 ? (j & 1) : PAR;
-    step(j);
+    auto load_kv = [&](int c) {
+      if (c < kLoads)
+        dma.issue_one(K + kbase, BN * (j + 2), sK + PAR * TE, c);
+      else if (c < 2 * kLoads)
+        dma.issue_one(V + kbase, BN * (j + 1), sV + (1 - PAR) * TE, c - kLoads);
+    };
+    if constexpr (SPREAD) {
+      wait_vmem_le<0>();
+      __syncthreads();
+    } else {
+      step(j);
+    }
     // the rare O rescale goes first, so that both phases form one basic
     // block for the scheduler
     if (rescale) rescale_o();
-    qk(sK + kbuf * TE, nx);
+    if constexpr (SPREAD)
+      qk(sK + kbuf * TE, nx, load_kv);
+    else
+      qk(sK + kbuf * TE, nx, no_load);
     exp_cvt(cur);
     sched_phase1();
     pv(sV + vbuf * TE);
@@ -467,7 +512,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fwd_bf16_pipe_kernel(
   else
     wait_vmem_le<Dma::kLoads>();
   __syncthreads();
-  qk(sK, sa);
+  qk(sK, sa, no_load);
   if (last == 0 && mask_last) mask_tile(sa, 0);
   row_max(sa, true);
 
@@ -476,22 +521,32 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fwd_bf16_pipe_kernel(
   using Even = std::integral_constant<int, 0>;
   using Odd = std::integral_constant<int, 1>;
   using Any = std::integral_constant<int, -1>;
+  // In the pair loop (j + 1 < last - 1) the pairs loaded, up to K_{last},
+  // all exist; they lie inside Lk when the workgroup's key range ends on a
+  // tile boundary.
   int j = 0;
-  for (; j + 1 < last - 1; j += 2) {
-    body(j, sa, sb, std::false_type{}, Even{});
-    body(j + 1, sb, sa, std::false_type{}, Odd{});
+  if (kend % BN == 0) {
+    for (; j + 1 < last - 1; j += 2) {
+      body(j, sa, sb, std::false_type{}, Even{}, std::true_type{});
+      body(j + 1, sb, sa, std::false_type{}, Odd{}, std::true_type{});
+    }
+  } else {
+    for (; j + 1 < last - 1; j += 2) {
+      body(j, sa, sb, std::false_type{}, Even{}, std::false_type{});
+      body(j + 1, sb, sa, std::false_type{}, Odd{}, std::false_type{});
+    }
   }
   if (j < last - 1) {
-    body(j, sa, sb, std::false_type{}, Any{});
+    body(j, sa, sb, std::false_type{}, Any{}, std::false_type{});
     sa[0] = sb[0];
     sa[1] = sb[1];
     ++j;
   }
   if (last >= 1) {
     if (mask_last)
-      body(j, sa, sb, std::true_type{}, Any{});
+      body(j, sa, sb, std::true_type{}, Any{}, std::false_type{});
     else
-      body(j, sa, sb, std::false_type{}, Any{});
+      body(j, sa, sb, std::false_type{}, Any{}, std::false_type{});
     sa[0] = sb[0];
     sa[1] = sb[1];
   }
