@@ -102,12 +102,16 @@ __global__ __launch_bounds__(256) void attn_bwd_delta_kernel(const T* __restrict
 }
 
 // ------------------------------------------------------------------ bf16 dK, dV
-template <int D, bool CAUSAL>
+// MAT: also store dS for attn_bwd_dq_gemm_kernel, as one 2 KB image per
+// (32 keys, 32 queries) block (see ds_image_row); query tiles a wave skips
+// (all of its keys after all of the tile's queries) are stored as zeros.
+// Requires Lq, Lk multiples of the key tile.
+template <int D, bool CAUSAL, bool MAT>
 __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_bf16_kernel(
     const u16* __restrict__ Q, const u16* __restrict__ K, const u16* __restrict__ V,
     const u16* __restrict__ dO, const float* __restrict__ L2, const float* __restrict__ NDelta,
-    u16* __restrict__ dK, u16* __restrict__ dV, int Lq, int Lk, int BH, int nkt, int group, float sl2,
-    float scale) {
+    u16* __restrict__ dK, u16* __restrict__ dV, u16* __restrict__ dST, int Lq, int Lk, int BH, int nkt,
+    int group, float sl2, float scale) {
   using Tile = SwzTile<D>;
   constexpr int NW = bwd_nw(D), BN = 32 * NW, BQ = dkdv_bq(D), MT = BQ / 32, S = kBwdStages;
   constexpr int NC = D / 16, ND = D / 32;
@@ -149,6 +153,18 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_b
   // K operand of chunk c (each lane reads back only what it parked itself)
   auto kop = [&](int c) {
     return c < KR ? kf[c] : *reinterpret_cast<const bf16x8*>(&sKf[((c - KR) * NW + w) * 512 + 8 * l]);
+  };
+  // dS image of (this wave's 32 keys, the 32 queries at q): this lane's 16
+  // accumulator values, 32 contiguous bytes at row ds_image_row(l) of image
+  // ((bh, q / 128, key / 32), (q / 32) % 4).  Stored non-temporal: the dQ
+  // GEMM reads it back from HBM.
+  u16* const dsimg = MAT ? dST + (((int64_t)bh * (Lq / 128)) * (Lk / 32) + key / 32) * 4096 + 16 * ds_image_row(l)
+                         : nullptr;
+  auto store_ds = [&](int q, const bf16x8 (&db)[2]) {
+    typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+    u16* p = dsimg + ((int64_t)(q / 128) * (Lk / 32)) * 4096 + (q / 32 % 4) * 1024;
+    __builtin_nontemporal_store(__builtin_bit_cast(u32x4, db[0]), reinterpret_cast<u32x4*>(p));
+    __builtin_nontemporal_store(__builtin_bit_cast(u32x4, db[1]), reinterpret_cast<u32x4*>(p + 8));
   };
   f32x16 adk[ND], adv[ND];
 #pragma unroll
@@ -226,6 +242,7 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_b
           db[r >> 3][r & 7] = (__bf16)(p * dp[r]);
         }
       }
+      if constexpr (MAT) store_ds(qb + 32 * mt, db);
       // dV^T += dO^T P and dK^T += Q^T dS over the 32 queries of this half:
       // k-chunk h holds queries 32mt + 16h + perm16 order.
       bf16x8 ov[2], oq[2];
@@ -255,7 +272,14 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_b
         wait_vmem_tiles<IPT>(issued - 1 - j);
       __syncthreads();
       issue_next();
-      if (CAUSAL && qb + BQ - 1 < wk_lo) continue;  // every query of the tile precedes every key of the wave
+      if (CAUSAL && qb + BQ - 1 < wk_lo) {  // every query of the tile precedes every key of the wave
+        if constexpr (MAT) {
+          const bf16x8 zero[2] = {bf16x8{}, bf16x8{}};
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) store_ds(qb + 32 * mt, zero);
+        }
+        continue;
+      }
       const int b = j % S;
       step(qb, sQ + b * TE, sdO + b * TE, sL + b * VS, sDl + b * VS, mask_tag);
     }
@@ -434,6 +458,122 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dq_bf1
   }
 }
 
+// ------------------------------------------------------------------ bf16 dQ from stored dS
+// dQ = s dS K as one GEMM over the dS the dK/dV kernel stored, so dQ needs
+// no recompute of S and dP.  dS is stored as 2 KB images, one per (32 keys,
+// 32 queries) block, in [BH][Lq/128][Lk/32][4] order (the images one
+// workgroup reads form one contiguous stream): the dK/dV accumulator
+// registers as they are (lane l = key l % 32 of queries with g = l / 32;
+// register r = query 8(r/4) + 4g + r%4), row l at row ds_image_row(l).
+//
+// Workgroup = 4 waves x 32 queries = DQG_BM queries (one dK/dV key tile wide,
+// so every block it reads was written; above the diagonal as zeros).  Stages
+// of 32 keys (K rows, and the 4 dS images of the workgroup's queries, 8 KB
+// contiguous) stream through a TT_DQG_STAGES-deep LDS ring.  Per stage and
+// wave dQ^T (d x 32 queries) += K^T dS^T, both operands by LDS transpose
+// reads.  The dS operand puts query q(n) = 8(n%16 / 4) + 4(n / 16 % 2) + n % 4
+// of the wave's 32 in MFMA column n and keys in natural order (the K^T
+// operand reads its rows in the same order); output rows follow q(n).
+// Requires Lq, Lk multiples of DQG_BM.
+constexpr int DQG_BM = 128;
+constexpr int DQG_BN = 32;  // keys per stage
+#ifndef TT_DQG_STAGES
+#define TT_DQG_STAGES 4
+#endif
+constexpr size_t kMaxDsBytes = size_t(8) << 30;  // largest dS workspace (bf16, Lq x Lk per head)
+
+template <int D, bool CAUSAL>
+__global__ __launch_bounds__(256, 2) void attn_bwd_dq_gemm_kernel(const u16* __restrict__ K,
+                                                                  const u16* __restrict__ dS,
+                                                                  u16* __restrict__ dQ, int Lq, int Lk, int BH,
+                                                                  int nqt, int group, float scale) {
+  constexpr int NW = 4, BM = DQG_BM, BN = DQG_BN, ND = D / 32, S = TT_DQG_STAGES;
+  static_assert(S >= 2 && S <= 4, "ring depth 2..4");
+  using KTile = SwzTile<D>;
+  constexpr int KE = KTile::kElems(BN), SE = (BM / 32) * 1024;  // elements per stage
+  using KDma = TileDma<D, BN, NW>;
+  constexpr int SL = SE / (NW * 512);  // dS load instructions per wave per stage (1 KB each)
+  constexpr int PER = KDma::kLoads + SL;
+  __shared__ __align__(16) u16 sK[S * KE];
+  __shared__ __align__(16) u16 sS[S * SE];
+
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l = threadIdx.x & 63, g = l >> 5;
+  int qt, bh;
+  map_tile(blockIdx.x, nqt, BH, group, qt, bh, CAUSAL);
+  const int q0 = qt * BM;
+  const int64_t kbase = (int64_t)bh * Lk * D;
+  // images of key block n and the workgroup's 4 query blocks: 8 KB at simg + 4096 n
+  const u16* simg = dS + ((int64_t)bh * (Lq / BM) + qt) * (Lk / 32) * 4096;
+
+  // Transpose reads: lane s of each 16-lane group points at row base + s / 4,
+  // 8-byte piece s % 4; the group then receives 4 consecutive rows of 16
+  // columns.  K^T operand of key chunk kc, half g: keys 16kc + 8g + (0..3)
+  // and 16kc + 8g + 4 + (0..3), d columns 32dt + 16G + (0..15).  dS operand:
+  // image rows 32G + the same keys, all 16 register columns.
+  const int t16 = l & 15, G = (l >> 4) & 1;
+  const int krow = 8 * g + (t16 >> 2), kcol = 16 * G + 4 * (t16 & 3);
+  const int srow = 32 * G + 8 * g, scol = 4 * (t16 & 3);
+
+  f32x16 acc[ND];
+#pragma unroll
+  for (int dt = 0; dt < ND; ++dt) acc[dt] = f32x16{};
+
+  const int ntiles = (CAUSAL ? min(Lk, q0 + BM) : Lk) / BN;
+  KDma kdma;
+  kdma.init();
+  int issued = 0;
+  auto issue_next = [&]() {
+    if (issued < ntiles) {
+      const int b = issued % S;
+      kdma.issue(K + kbase, BN * issued, Lk, sK + b * KE);
+      const u16* src = simg + (int64_t)issued * 4096;
+      const uint32_t lds = lds_addr(sS + b * SE);
+#pragma unroll
+      for (int i = 0; i < SL; ++i) {
+        const uint32_t off = 1024u * (uint32_t)(i * NW + w);
+        glds16(src, off + 16u * (uint32_t)l, lds + off);
+      }
+      ++issued;
+    }
+  };
+  for (int s0 = 0; s0 < S - 1; ++s0) issue_next();
+  for (int n = 0; n < ntiles; ++n) {
+    wait_vmem_tiles<PER>(issued - 1 - n);  // tiles n + 1 .. issued - 1 may stay in flight
+    __syncthreads();
+    issue_next();
+    const u16* tK = sK + (n % S) * KE;
+    const u16* tS = sS + (n % S) * SE + w * 1024;  // this wave's query block
+#pragma unroll
+    for (int kc = 0; kc < BN / 16; ++kc) {
+      const int sr = srow + 16 * kc;  // a multiple of 4; rows sr .. sr + 3 and sr + 4 .. sr + 7
+      const bf16x8 b = lds_read_tr16x2(&tS[16 * (ds_image_row(sr) + (t16 >> 2)) + scol],
+                                       &tS[16 * (ds_image_row(sr + 4) + (t16 >> 2)) + scol]);
+#pragma unroll
+      for (int dt = 0; dt < ND; ++dt) {
+        const int r0 = 16 * kc + krow;
+        const bf16x8 a =
+            lds_read_tr16x2(&tK[KTile::at4(r0, 32 * dt + kcol)], &tK[KTile::at4(r0 + 4, 32 * dt + kcol)]);
+        acc[dt] = mfma_bf16_32x32x16(a, b, acc[dt]);
+      }
+    }
+  }
+  wait_vmem_le<0>();  // nothing may be in flight into LDS when the workgroup exits
+
+  const int n = l & 31;
+  const int q = q0 + 32 * w + 8 * ((n & 15) >> 2) + 4 * ((n >> 4) & 1) + (n & 3);
+  u16* row = dQ + ((int64_t)bh * Lq + q) * D;
+#pragma unroll
+  for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+    for (int r = 0; r < 16; r += 4) {
+      uint2 v;
+      v.x = pack_bf16x2(acc[dt][r] * scale, acc[dt][r + 1] * scale);
+      v.y = pack_bf16x2(acc[dt][r + 2] * scale, acc[dt][r + 3] * scale);
+      *reinterpret_cast<uint2*>(row + 32 * dt + acc_row(r, g)) = v;
+    }
+}
+
 // ------------------------------------------------------------------ launchers
 template <typename T, int D, bool CAUSAL>
 static int launch_bwd(const T* q, const T* k, const T* v, const T* o, const float* lse, const T* dout,
@@ -460,8 +600,30 @@ static int launch_bwd(const T* q, const T* k, const T* v, const T* o, const floa
     if (nkt * BH > 0x7fffffff || nqt * BH > 0x7fffffff) return fail(TT_ERR_ARG, "attention backward: grid too large");
     // heads in flight per XCD: tiles for the resident workgroups of its 32 CUs
     const int gk = pick_group(BH, nkt, 32 * 8 / NW), gq = pick_group(BH, nqt, 32 * 8 / NW);
-    hipLaunchKernelGGL((attn_bwd_dkdv_bf16_kernel<D, CAUSAL>), dim3((unsigned)(nkt * BH)), dim3(64 * NW), 0, st,
-                       q, k, v, dout, l2, delta, dk, dv, (int)Lq, (int)Lk, (int)BH, (int)nkt, gk, sl2, scale);
+    // dQ: one GEMM over the stored dS when the tiles are full and the dS
+    // workspace stays under kMaxDsBytes; otherwise recompute S and dP.
+    if constexpr (D >= 64) {
+      const size_t ds_bytes = (size_t)BH * (size_t)Lk * (size_t)Lq * sizeof(u16);
+      const bool mat = 32 * NW == DQG_BM && Lq % DQG_BM == 0 && Lk % DQG_BM == 0 &&
+                       Lq <= (int64_t(1) << 24) && ds_bytes <= kMaxDsBytes;
+      if (mat) {
+        u16* ds = nullptr;
+        if ((rc = workspace(2, ds_bytes, (void**)&ds))) return rc;
+        hipLaunchKernelGGL((attn_bwd_dkdv_bf16_kernel<D, CAUSAL, true>), dim3((unsigned)(nkt * BH)), dim3(64 * NW),
+                           0, st, q, k, v, dout, l2, delta, dk, dv, ds, (int)Lq, (int)Lk, (int)BH, (int)nkt, gk, sl2,
+                           scale);
+        TT_LAUNCHED("attention backward dK/dV launch", st);
+        const int64_t nqg = Lq / DQG_BM;
+        const int gg = pick_group(BH, nqg, 32 * 2);
+        hipLaunchKernelGGL((attn_bwd_dq_gemm_kernel<D, CAUSAL>), dim3((unsigned)(nqg * BH)), dim3(256), 0, st, k, ds,
+                           dq, (int)Lq, (int)Lk, (int)BH, (int)nqg, gg, scale);
+        TT_LAUNCHED("attention backward dQ launch", st);
+        return ok();
+      }
+    }
+    hipLaunchKernelGGL((attn_bwd_dkdv_bf16_kernel<D, CAUSAL, false>), dim3((unsigned)(nkt * BH)), dim3(64 * NW), 0,
+                       st, q, k, v, dout, l2, delta, dk, dv, nullptr, (int)Lq, (int)Lk, (int)BH, (int)nkt, gk, sl2,
+                       scale);
     TT_LAUNCHED("attention backward dK/dV launch", st);
     hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<D, CAUSAL>), dim3((unsigned)(nqt * BH)), dim3(64 * NW), 0, st,
                        q, k, v, dout, l2, delta, dq, (int)Lq, (int)Lk, (int)BH, (int)nqt, gq, sl2, scale);

@@ -87,13 +87,6 @@ __device__ __forceinline__ float sum_bf16x2(const bf16x8& v, int e, float acc) {
   return __builtin_amdgcn_fdot2_f32_bf16(pair, one, acc, false);
 }
 
-// Keep an MFMA accumulator in AGPRs: an empty asm that takes the value in
-// AGPRs.  Kernels built with VGPR-form MFMAs (-amdgpu-mfma-vgpr-form) then
-// give the accumulating MFMA an AGPR destination and source C, leaving the
-// VGPRs to the operands and the score tiles the VALU works on.  It emits no
-// instruction, so the compiler's MFMA hazard handling is unaffected.
-__device__ __forceinline__ void pin_agpr(f32x16& acc) { asm volatile("" : "+a"(acc)); }
-
 // Instruction classes of __builtin_amdgcn_sched_group_barrier.
 constexpr int kSchedMFMA = 0x008;
 constexpr int kSchedVALU = 0x002 | 0x400;  // VALU incl. transcendental
@@ -250,6 +243,13 @@ struct TileDma {
     }
   }
 };
+
+// Row position of row l (0..63) of a 2 KB dS image (64 rows of 32 bytes):
+// bit 2 flipped in rows 8..15 of every 16, so that the four 4-row groups a
+// transpose read touches (rows 0-3, 8-11, 32-35, 40-43 plus a multiple of
+// 4) spread over both halves of the LDS banks.  An involution that keeps
+// groups of 4 consecutive rows (starting at a multiple of 4) together.
+__device__ __forceinline__ constexpr int ds_image_row(int l) { return l ^ (((l >> 3) & 1) << 2); }
 
 // s_waitcnt vmcnt(N): wait until at most N of this wave's global loads are
 // outstanding (loads retire in order), LDS / export counters untouched.
