@@ -48,10 +48,10 @@ C4 = dict(B=64, H=32, Lkv=8192, d=128)
 # write x1.000); the commands and raw counters are in
 # profiles/hbm_traffic_c5_c4.md.  Re-measured whenever a kernel changes.
 MEASURED_TRAFFIC_MIB = {
-    "attn_fwd": 574.7,
+    "attn_fwd": 524.9,
     "attn_bwd_delta": 264.0,
-    "attn_bwd_dkdv": 862.1,
-    "attn_bwd_dq": 768.1,
+    "attn_bwd_dkdv": 3130.6,   # includes the 2.06 GiB of dS it stores for the dQ GEMM
+    "attn_bwd_dq": 2571.3,     # the dQ GEMM: reads that dS back
     "attn_decode_split": 8217.7,
 }
 
@@ -261,7 +261,11 @@ def main(argv=None):
         kernels = {}
         for n, t in per.items():
             tf = kf[n] / (t * 1e-3) / 1e12 if kf[n] else None
-            kernels[n] = {"avg_ms": t, "tflops": tf, "frac": (tf / PEAK_BF16_TFLOPS) if tf else None}
+            tb = traffic_bytes(n)
+            kernels[n] = {"avg_ms": t, "tflops": tf, "frac": (tf / PEAK_BF16_TFLOPS) if tf else None,
+                          # measured HBM bytes per launch over this launch time: the dQ GEMM
+                          # (one GEMM unit over 2 GiB of stored dS) is bound by this, not MFMA
+                          "hbm_gbs": (tb / (t * 1e-3) / 1e9) if tb else None}
         out["kernels"] = kernels
         dom = max(per, key=per.get)
         ach = kf[dom] / (per[dom] * 1e-3) / 1e12

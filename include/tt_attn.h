@@ -144,7 +144,12 @@ int tt_attn_fwd_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v, ui
  * through MatMul.gradient (:421-429), Transpose.gradient (:338-340),
  * MulScalar.gradient (:241-242), EWiseDiv.gradient (:296-298),
  * BroadcastTo/Summation.gradient (:373-380, :400-408), Exp.gradient (:469-470).
- * Uses a library-owned scratch buffer of B*H*Lq floats (the row sums D). */
+ * Uses a library-owned scratch buffer of 2*B*H*Lq floats (-D and LSE*log2(e)).
+ * The bf16 entry point, for d in {64, 128} with Lq and Lk multiples of 128,
+ * also stores dS (bf16, B*H*Lq*Lk elements, at most 8 GiB) in a library-owned
+ * workspace and computes dQ = s dS K from it as one GEMM; other shapes
+ * recompute S and dP for dQ.  Results agree either way (dS enters the dQ
+ * MFMA as bf16 in both). */
 int tt_attn_bwd_f32(const float* q, const float* k, const float* v, const float* o,
                     const float* lse, const float* do_, float* dq, float* dk, float* dv,
                     int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t d,

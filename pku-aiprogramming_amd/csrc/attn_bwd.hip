@@ -51,7 +51,10 @@ static_assert(kBwdStages >= 2 && kBwdStages <= 4, "tile ring depth must be 2..4"
 constexpr int DQ_BN = 64;  // keys per LDS tile of the dQ kernel
 // Query rows per LDS tile of the dK/dV kernel: the ring of Q / dO tiles
 // plus the V rows of the workgroup fit 160 KB of LDS.
-constexpr int dkdv_bq(int D) { return D == 128 ? 32 : 64; }
+#ifndef TT_DKDV_BQ128
+#define TT_DKDV_BQ128 32
+#endif
+constexpr int dkdv_bq(int D) { return D == 128 ? TT_DKDV_BQ128 : 64; }
 // K chunks (16 columns each) the dK/dV kernel keeps in LDS rather than in
 // registers.  At d = 128 the dK / dV accumulators (128 VGPRs) and the K rows
 // (32) leave too little of the 256 registers of a 2-waves-per-SIMD kernel;
@@ -604,7 +607,7 @@ static int launch_bwd(const T* q, const T* k, const T* v, const T* o, const floa
     // workspace stays under kMaxDsBytes; otherwise recompute S and dP.
     if constexpr (D >= 64) {
       const size_t ds_bytes = (size_t)BH * (size_t)Lk * (size_t)Lq * sizeof(u16);
-      const bool mat = 32 * NW == DQG_BM && Lq % DQG_BM == 0 && Lk % DQG_BM == 0 &&
+      const bool mat = (32 * NW) % DQG_BM == 0 && Lq % DQG_BM == 0 && Lk % (32 * NW) == 0 &&
                        Lq <= (int64_t(1) << 24) && ds_bytes <= kMaxDsBytes;
       if (mat) {
         u16* ds = nullptr;
