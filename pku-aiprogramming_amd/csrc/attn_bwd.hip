@@ -124,17 +124,25 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_b
   constexpr int VS = 64;  // stride of the LSE / D row buffers (one 64-lane load each)
   using Dma = TileDma<D, BQ, NW>;
   constexpr int IPT = 2 * Dma::kLoads;  // Q + dO loads per wave per tile
-  // Ring of Q / dO tiles with their LSE (log2) / D rows, and the workgroup's
-  // V rows, all filled by direct global->LDS loads
-  __shared__ __align__(16) u16 sQ[S * TE];
-  __shared__ __align__(16) u16 sdO[S * TE];
-  __shared__ __align__(16) u16 sV[Tile::kElems(BN)];
-  __shared__ __align__(16) float sL[S * VS];
-  __shared__ __align__(16) float sDl[S * VS];
-  // parked K chunks, lane-linear: chunk KR + c of lane l of wave w at 16 (64 (c NW + w) + l) bytes
-  __shared__ __align__(16) u16 sKf[(KL > 0 ? KL : 1) * NW * 512];
+  // One LDS block, carved at fixed byte offsets so that every operand read
+  // is a per-lane address plus an immediate: the ring of Q / dO tiles with
+  // their LSE (log2) / D rows and the workgroup's V rows, all filled by direct
+  // global->LDS loads, then the parked K chunks (lane-linear: chunk KR + c of
+  // lane l of wave w at 16 (64 (c NW + w) + l) bytes).
+  constexpr int kOQ = 0, kOdO = kOQ + 2 * S * TE, kOV = kOdO + 2 * S * TE, kOL = kOV + 2 * Tile::kElems(BN),
+                kOD = kOL + 4 * S * VS, kOK = kOD + 4 * S * VS, kLds = kOK + (KL > 0 ? KL : 1) * NW * 1024;
+  static_assert(kOV <= 65536, "Q / dO ring offsets exceed the 16-bit LDS immediate");
+  __shared__ __align__(16) char smem[kLds];
+  u16* const sQ = reinterpret_cast<u16*>(smem + kOQ);
+  u16* const sdO = reinterpret_cast<u16*>(smem + kOdO);
+  u16* const sV = reinterpret_cast<u16*>(smem + kOV);
+  float* const sL = reinterpret_cast<float*>(smem + kOL);
+  float* const sDl = reinterpret_cast<float*>(smem + kOD);
+  u16* const sKf = reinterpret_cast<u16*>(smem + kOK);
+  const uint32_t a0 = lds_addr(smem);
 
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63, g = l >> 5, r32 = l & 31;
+  const int wu = __builtin_amdgcn_readfirstlane(w);  // w, known wave-uniform (scalar branches)
   int kt, bh;
   map_tile(blockIdx.x, nkt, BH, group, kt, bh, false);  // causal: key tile 0 sees every query
   const int k0 = kt * BN;
@@ -154,9 +162,8 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_b
     for (int c = KR; c < NC; ++c) *reinterpret_cast<bf16x8*>(&sKf[((c - KR) * NW + w) * 512 + 8 * l]) = kf[c];
   }
   // K operand of chunk c (each lane reads back only what it parked itself)
-  auto kop = [&](int c) {
-    return c < KR ? kf[c] : *reinterpret_cast<const bf16x8*>(&sKf[((c - KR) * NW + w) * 512 + 8 * l]);
-  };
+  uint32_t kofs = a0 + kOK + 16 * (64 * w + l);
+  auto kop = [&](int c) { return c < KR ? kf[c] : lds_ld<bf16x8>(kofs + (c - KR) * NW * 1024); };
   // dS image of (this wave's 32 keys, the 32 queries at q): this lane's 16
   // accumulator values, 32 contiguous bytes at row ds_image_row(l) of image
   // ((bh, q / 128, key / 32), (q / 32) % 4).  Stored non-temporal: the dQ
@@ -190,7 +197,7 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_b
       const int b = issued % S, qb = qstart + issued * BQ;
       dma.issue(Q + qbase, qb, Lq, sQ + b * TE);
       dma.issue(dO + qbase, qb, Lq, sdO + b * TE);
-      if (w == 0) {
+      if (wu == 0) {
         load_vec_lds(L2 + lbase + qb, Lq - qb, sL + b * VS);
         load_vec_lds(NDelta + lbase + qb, Lq - qb, sDl + b * VS);
       }
@@ -198,7 +205,27 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_b
     }
   };
 
-  auto step = [&](int qb, const u16* tQ, const u16* tdO, const float* tL, const float* tD, auto mask_tag) {
+  // This lane's LDS byte addresses in Q buffer 0 (dO, other buffers and query
+  // halves are immediates away), all loop invariant: 16-byte row reads
+  // (chunk 2c + g of row r32; half mt adds 32 rows), the wave's V rows,
+  // transpose reads at rows trow / trow + 8 of column 32 dt + tcol (half h
+  // adds 16 rows), and the LSE / D rows.  The swizzle depends on the low four
+  // row bits only, so those row offsets are plain immediates.
+  uint32_t roff[NC], voff[NC], troff[2][ND];
+  uint32_t lofs = a0 + kOL + 16 * g;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    roff[c] = a0 + kOQ + 2 * Tile::chunk(r32, 2 * c + g);
+    voff[c] = a0 + kOV + 2 * Tile::chunk(32 * w + r32, 2 * c + g);
+  }
+#pragma unroll
+  for (int dt = 0; dt < ND; ++dt) {
+    troff[0][dt] = a0 + kOQ + 2 * Tile::at4(trow, 32 * dt + tcol);
+    troff[1][dt] = a0 + kOQ + 2 * Tile::at4(trow + 8, 32 * dt + tcol);
+  }
+
+  // Tile in ring buffer b: bq = b * (Q tile bytes), bl = b * (LSE row bytes).
+  auto step = [&](int qb, int bq, int bl, auto mask_tag) __attribute__((always_inline)) {
     constexpr bool MASK = decltype(mask_tag)::value;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
@@ -207,7 +234,7 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_b
       f32x16 s = f32x16{}, dp;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const float4 nd = *reinterpret_cast<const float4*>(&tD[32 * mt + 8 * j + 4 * g]);
+        const f32x4 nd = lds_ld<f32x4>(lofs + (kOD - kOL) + bl + 128 * mt + 32 * j);
         dp[4 * j] = nd.x;
         dp[4 * j + 1] = nd.y;
         dp[4 * j + 2] = nd.z;
@@ -215,23 +242,23 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_b
       }
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
-        const int off = Tile::chunk(32 * mt + r32, 2 * c + g);
-        s = mfma_bf16_32x32x16(*reinterpret_cast<const bf16x8*>(&tQ[off]), kop(c), s);
-        const bf16x8 vb = *reinterpret_cast<const bf16x8*>(&sV[Tile::chunk(32 * w + r32, 2 * c + g)]);
-        dp = mfma_bf16_32x32x16(*reinterpret_cast<const bf16x8*>(&tdO[off]), vb, dp);
+        const uint32_t off = roff[c] + bq + 64 * mt * D;
+        s = mfma_bf16_32x32x16(lds_ld<bf16x8>(off), kop(c), s);
+        const bf16x8 vb = lds_ld<bf16x8>(voff[c]);
+        dp = mfma_bf16_32x32x16(lds_ld<bf16x8>(off + (kOdO - kOQ)), vb, dp);
       }
       // transposed dO / Q operands of dV^T / dK^T MFMA i = h * ND + dt,
       // fetched one MFMA pair ahead
-      auto tr_op = [&](const u16* tile_, int i) {
-        const int r0 = 32 * mt + 16 * (i / ND) + trow, col = 32 * (i % ND) + tcol;
-        return lds_read_tr16x2(&tile_[Tile::at4(r0, col)], &tile_[Tile::at4(r0 + 8, col)]);
+      auto tr_op = [&](int tile_off, int i) {
+        const uint32_t o = tile_off + bq + 2 * (32 * mt + 16 * (i / ND)) * D;
+        return lds_tr16x2_at(troff[0][i % ND] + o, troff[1][i % ND] + o);
       };
       // s[r] = S[query qb + 32mt + acc_row(r, g)][key]
       bf16x8 pb[2], db[2];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int qi = 32 * mt + 8 * j + 4 * g;  // rows acc_row(4j..4j+3, g)
-        const float4 lv = *reinterpret_cast<const float4*>(&tL[qi]);
+        const f32x4 lv = lds_ld<f32x4>(lofs + bl + 128 * mt + 32 * j);
         const float la[4] = {lv.x, lv.y, lv.z, lv.w};
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
@@ -249,13 +276,13 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_b
       // dV^T += dO^T P and dK^T += Q^T dS over the 32 queries of this half:
       // k-chunk h holds queries 32mt + 16h + perm16 order.
       bf16x8 ov[2], oq[2];
-      ov[0] = tr_op(tdO, 0);
-      oq[0] = tr_op(tQ, 0);
+      ov[0] = tr_op(kOdO - kOQ, 0);
+      oq[0] = tr_op(0, 0);
 #pragma unroll
       for (int i = 0; i < 2 * ND; ++i) {
         if (i + 1 < 2 * ND) {
-          ov[(i + 1) & 1] = tr_op(tdO, i + 1);
-          oq[(i + 1) & 1] = tr_op(tQ, i + 1);
+          ov[(i + 1) & 1] = tr_op(kOdO - kOQ, i + 1);
+          oq[(i + 1) & 1] = tr_op(0, i + 1);
         }
         adv[i % ND] = mfma_bf16_32x32x16(ov[i & 1], pb[i / ND], adv[i % ND]);
         adk[i % ND] = mfma_bf16_32x32x16(oq[i & 1], db[i / ND], adk[i % ND]);
@@ -267,24 +294,68 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_b
   // ragged) and unmasked query tiles run in separate loops so that neither
   // loop switches the accumulators' registers.
   int j = 0;
-  auto run = [&](int lo, int hi, auto mask_tag) {
-    for (int qb = lo; qb < hi; qb += BQ, ++j) {
-      if (w == 0)
-        wait_vmem_tiles<IPT + 2>(issued - 1 - j);
-      else
-        wait_vmem_tiles<IPT>(issued - 1 - j);
-      __syncthreads();
-      issue_next();
-      if (CAUSAL && qb + BQ - 1 < wk_lo) {  // every query of the tile precedes every key of the wave
+  // tile j at qb in ring buffer b (b < 0: j % S at run time)
+  auto tile_at = [&](int qb, auto b_tag, auto mask_tag) __attribute__((always_inline)) {
+    if (wu == 0)
+      wait_vmem_tiles<IPT + 2, S - 1>(issued - 1 - j);
+    else
+      wait_vmem_tiles<IPT, S - 1>(issued - 1 - j);
+    __syncthreads();
+    issue_next();
+    if constexpr (CAUSAL && decltype(mask_tag)::value) {
+      if (qb + BQ - 1 < wk_lo) {  // every query of the tile precedes every key of the wave
         if constexpr (MAT) {
           const bf16x8 zero[2] = {bf16x8{}, bf16x8{}};
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt) store_ds(qb + 32 * mt, zero);
         }
-        continue;
+        return;
       }
-      const int b = j % S;
-      step(qb, sQ + b * TE, sdO + b * TE, sL + b * VS, sDl + b * VS, mask_tag);
+    }
+    constexpr int bc = decltype(b_tag)::value;
+    const int b = bc >= 0 ? bc : j % S;
+    // keep address + immediate addressing (no hoisted per-buffer copies)
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      opaque(roff[c]);
+      opaque(voff[c]);
+    }
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt) {
+      opaque(troff[0][dt]);
+      opaque(troff[1][dt]);
+    }
+    opaque(lofs);
+    opaque(kofs);
+    step(qb, b * 2 * TE, b * 4 * VS, mask_tag);
+  };
+  using AnyBuf = std::integral_constant<int, -1>;
+  auto run = [&](int lo, int hi, auto mask_tag) __attribute__((always_inline)) {
+    for (int qb = lo; qb < hi; qb += BQ, ++j) tile_at(qb, AnyBuf{}, mask_tag);
+  };
+  // Unmasked tiles (no query precedes a key of the workgroup): with a
+  // two-buffer ring the loop is unrolled by buffer, so every LDS address is
+  // a loop-invariant lane offset plus an immediate.
+  auto run_full = [&](int lo, int hi) __attribute__((always_inline)) {
+    if constexpr (S == 2) {
+      int qb = lo;
+      if ((j & 1) && qb < hi) {
+        tile_at(qb, std::integral_constant<int, 1>{}, std::false_type{});
+        qb += BQ;
+        ++j;
+      }
+      for (; qb + BQ < hi; qb += 2 * BQ) {
+        tile_at(qb, std::integral_constant<int, 0>{}, std::false_type{});
+        ++j;
+        tile_at(qb + BQ, std::integral_constant<int, 1>{}, std::false_type{});
+        ++j;
+      }
+      if (qb < hi) {
+        tile_at(qb, std::integral_constant<int, 0>{}, std::false_type{});
+        ++j;
+      }
+    } else {
+      run(lo, hi, std::false_type{});
     }
   };
   // The V tile is issued first, so the first wait (which leaves at most the
@@ -302,7 +373,7 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_b
   const int qfull = (Lq / BQ) * BQ;
   const int qdiag = CAUSAL ? min(k0 + BN, Lq) : qstart;  // [qstart, qdiag): tiles crossing the diagonal
   run(qstart, qdiag, std::true_type{});
-  run(qdiag, qfull, std::false_type{});
+  run_full(qdiag, qfull);
   run(max(qdiag, qfull), Lq, std::true_type{});
   wait_vmem_le<0>();  // nothing may be in flight into LDS when the workgroup exits
 

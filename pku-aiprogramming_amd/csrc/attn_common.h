@@ -120,6 +120,24 @@ __device__ __forceinline__ bf16x8 lds_read_tr16x2(const u16* p0, const u16* p1) 
 
 __device__ __forceinline__ bool wave_any(bool p) { return __any(p); }
 
+// Redefines x in place with no instruction, so loop-invariant code motion
+// cannot hoist (x + constant) out of a loop into a second register: the
+// constant then folds into the memory instruction's offset field.
+__device__ __forceinline__ void opaque(uint32_t& x) { asm volatile("" : "+v"(x)); }
+
+// LDS reads at a byte address (as lds_addr returns).
+template <typename V>
+__device__ __forceinline__ V lds_ld(uint32_t a) {
+  return *(const __attribute__((address_space(3))) V*)(uintptr_t)a;
+}
+__device__ __forceinline__ bf16x8 lds_tr16x2_at(uint32_t a0, uint32_t a1) {
+  s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(uintptr_t)a0);
+  s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(uintptr_t)a1);
+  typedef short s16x8 __attribute__((ext_vector_type(8)));
+  s16x8 v = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+  return __builtin_bit_cast(bf16x8, v);
+}
+
 // Dense row-major bf16 tile of D columns in LDS, addressed by 16-byte
 // chunks, that serves two read patterns without bank conflicts:
 //   * 16-byte row reads: 16 lanes read one chunk of 16 consecutive rows;
@@ -258,12 +276,14 @@ __device__ __forceinline__ void wait_vmem_le() {
   static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
-// Runtime count in [0, 3 * PER]: wait until at most n * PER loads remain.
-template <int PER>
+// Runtime count n in [0, MAXN] (MAXN <= 3): wait until at most n * PER
+// loads remain.
+template <int PER, int MAXN = 3>
 __device__ __forceinline__ void wait_vmem_tiles(int n) {
-  if (n >= 3) wait_vmem_le<3 * PER>();
-  else if (n == 2) wait_vmem_le<2 * PER>();
-  else if (n == 1) wait_vmem_le<PER>();
+  static_assert(MAXN >= 0 && MAXN <= 3, "at most 3 tiles in flight");
+  if (MAXN >= 3 && n >= 3) wait_vmem_le<(MAXN >= 3 ? 3 : 0) * PER>();
+  else if (MAXN >= 2 && n == 2) wait_vmem_le<(MAXN >= 2 ? 2 : 0) * PER>();
+  else if (MAXN >= 1 && n == 1) wait_vmem_le<(MAXN >= 1 ? 1 : 0) * PER>();
   else wait_vmem_le<0>();
 }
 
