@@ -124,6 +124,7 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_b
   constexpr int VS = 64;  // stride of the LSE / D row buffers (one 64-lane load each)
   using Dma = TileDma<D, BQ, NW>;
   constexpr int IPT = 2 * Dma::kLoads;  // Q + dO loads per wave per tile
+  constexpr int kStores = MAT ? 2 * MT : 0;  // dS image stores per wave per tile
   // One LDS block, carved at fixed byte offsets so that every operand read
   // is a per-lane address plus an immediate: the ring of Q / dO tiles with
   // their LSE (log2) / D rows and the workgroup's V rows, all filled by direct
@@ -170,9 +171,11 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_b
   // GEMM reads it back from HBM.
   u16* const dsimg = MAT ? dST + (((int64_t)bh * (Lq / 128)) * (Lk / 32) + key / 32) * 4096 + 16 * ds_image_row(l)
                          : nullptr;
+  const int64_t img_row = (int64_t)(Lk / 32) * 4096;  // elements per 128 query rows of dS images
   auto store_ds = [&](int q, const bf16x8 (&db)[2]) {
     typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
-    u16* p = dsimg + ((int64_t)(q / 128) * (Lk / 32)) * 4096 + (q / 32 % 4) * 1024;
+    const unsigned uq = q;  // q >= 0: unsigned division is a shift
+    u16* p = dsimg + (int64_t)(uq / 128) * img_row + (uq / 32 % 4) * 1024;
     __builtin_nontemporal_store(__builtin_bit_cast(u32x4, db[0]), reinterpret_cast<u32x4*>(p));
     __builtin_nontemporal_store(__builtin_bit_cast(u32x4, db[1]), reinterpret_cast<u32x4*>(p + 8));
   };
@@ -194,7 +197,7 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_b
   int issued = 0;
   auto issue_next = [&]() {
     if (issued < ntiles) {
-      const int b = issued % S, qb = qstart + issued * BQ;
+      const int b = (unsigned)issued % S, qb = qstart + issued * BQ;
       dma.issue(Q + qbase, qb, Lq, sQ + b * TE);
       dma.issue(dO + qbase, qb, Lq, sdO + b * TE);
       if (wu == 0) {
@@ -296,10 +299,16 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_b
   int j = 0;
   // tile j at qb in ring buffer b (b < 0: j % S at run time)
   auto tile_at = [&](int qb, auto b_tag, auto mask_tag) __attribute__((always_inline)) {
-    if (wu == 0)
-      wait_vmem_tiles<IPT + 2, S - 1>(issued - 1 - j);
-    else
-      wait_vmem_tiles<IPT, S - 1>(issued - 1 - j);
+    if constexpr (S == 2) {
+      // In flight: this tile's loads (issued after the previous tile's
+      // barrier), then the previous tile's dS stores.  Loads and stores retire
+      // in issue order, so the stores need not drain here.
+      wait_vmem_le<kStores>();
+    } else if (wu == 0) {
+      wait_vmem_tiles<IPT + 2 + kStores, S - 1>(issued - 1 - j);
+    } else {
+      wait_vmem_tiles<IPT + kStores, S - 1>(issued - 1 - j);
+    }
     __syncthreads();
     issue_next();
     if constexpr (CAUSAL && decltype(mask_tag)::value) {
@@ -313,7 +322,7 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_b
       }
     }
     constexpr int bc = decltype(b_tag)::value;
-    const int b = bc >= 0 ? bc : j % S;
+    const int b = bc >= 0 ? bc : (unsigned)j % S;
     // keep address + immediate addressing (no hoisted per-buffer copies)
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
