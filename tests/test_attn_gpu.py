@@ -210,6 +210,12 @@ SHAPES = [
     (1, 1, 65, 300, 128, False),
     (2, 2, 257, 257, 32, True),
     (1, 1, 3, 1000, 64, False),
+    # d = 128 with Lq, Lk multiples of 128: the stored-dS backward (dQ as a
+    # GEMM over the dS images the dK / dV kernel writes)
+    (1, 2, 256, 256, 128, True),
+    (2, 1, 512, 512, 128, True),
+    (1, 1, 128, 512, 128, False),
+    (2, 1, 384, 256, 128, False),
 ]
 
 
