@@ -172,6 +172,38 @@ def run_copy(T, steps, warmup, nbytes=1 << 30):
     return ms, 2 * nbytes / (ms * 1e-3) / 1e9
 
 
+def run_gemm_ceiling(n=16384, iters=5):
+    """Library bf16 GEMM (torch -> hipBLASLt), n^3, on random N(0,1) and on all-ones
+    operands: the MFMA rate a tuned GEMM sustains on this box.  The instruction
+    stream is the same for both; the gap is the power the data toggles."""
+    import torch
+
+    res = {"gemm": f"bf16 {n}x{n}x{n}, torch.matmul (hipBLASLt)", "iters": iters}
+    g = torch.Generator(device="cuda").manual_seed(0)
+    for kind in ("random", "ones"):
+        if kind == "random":
+            a = torch.randn(n, n, device="cuda", dtype=torch.bfloat16, generator=g)
+            b = torch.randn(n, n, device="cuda", dtype=torch.bfloat16, generator=g)
+        else:
+            a = torch.ones(n, n, device="cuda", dtype=torch.bfloat16)
+            b = torch.ones(n, n, device="cuda", dtype=torch.bfloat16)
+        for _ in range(2):
+            c = a @ b
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(iters):
+            c = a @ b
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / iters
+        res[f"{kind}_tflops"] = 2.0 * n ** 3 / (ms * 1e-3) / 1e12
+        del a, b, c
+    torch.cuda.empty_cache()
+    res["random_frac_of_peak"] = res["random_tflops"] / PEAK_BF16_TFLOPS
+    return res
+
+
 def cpu_baseline(sample_heads):
     """The reference's op chain in float32 numpy on `sample_heads` heads of
     the headline workload (1 warm-up head, not counted)."""
@@ -217,8 +249,9 @@ def main(argv=None):
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", choices=["all", "fwdbwd", "decode", "copy"], default="all",
-                    help="run one workload only (for profiler runs; 'copy' is the 1 GiB calibration copy)")
+    ap.add_argument("--only", choices=["all", "fwdbwd", "decode", "copy", "ceiling"], default="all",
+                    help="run one workload only (for profiler runs; 'copy' is the 1 GiB calibration copy, "
+                         "'ceiling' the library bf16 GEMM reference)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-heads", type=int, default=128)
     args = ap.parse_args(argv)
@@ -228,6 +261,12 @@ def main(argv=None):
               "(heads and batch shard across GPUs with no exchange, so N GPUs run N independent shares).",
               file=sys.stderr)
         return 2
+
+    if args.only == "ceiling":
+        # before the library is loaded: torch brings its own HIP runtime
+        print(json.dumps({"metric": "library bf16 GEMM TFLOP/s (random vs all-ones operands)",
+                          **run_gemm_ceiling()}), flush=True)
+        return 0
 
     import tt_capi as T
 
@@ -291,6 +330,17 @@ def main(argv=None):
         if args.only == "decode":
             out["value"], out["unit"], out["ms_per_step"] = gbs, "GB/s", ms
             out["roofline"] = out["decode"]["roofline"]
+
+    if args.only == "all":
+        # context for roofline.frac: what a tuned library GEMM sustains on real data,
+        # measured in a child process (torch's HIP runtime is not the library's)
+        import subprocess
+        r = subprocess.run([sys.executable, os.path.abspath(__file__), "--only", "ceiling"],
+                           capture_output=True, text=True, timeout=300)
+        try:
+            out["mfma_ceiling"] = json.loads(r.stdout.strip().splitlines()[-1])
+        except (ValueError, IndexError):
+            out["mfma_ceiling"] = {"error": (r.stderr or "no output").strip().splitlines()[-1:]}
 
     if not args.no_cpu_baseline and args.cpu_heads > 0:
         out["cpu_baseline"] = cpu_baseline(args.cpu_heads)
