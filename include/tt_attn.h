@@ -173,6 +173,18 @@ int tt_attn_decode_f32(const float* q, const float* k, const float* v, float* o,
                        int64_t B, int64_t H, int64_t Lkv, int64_t d, float scale,
                        void* stream);
 
+/* ------------------------------------------------------------- softmax */
+
+/* Row softmax over the last axis of a row-major [rows, cols] fp32 matrix:
+ *   y[r][c] = exp(x[r][c] - m_r) / sum_c' exp(x[r][c'] - m_r),  m_r = max_c x[r][c].
+ * Replaces SoftmaxForward (src/Layers.cu:324-349: cudaChannelMax, Sub, Exp,
+ * Sum, Div of src/Layers_kernels.cu:189-257, the max and the sum each a host
+ * loop of thrust calls per row) with one kernel: rows up to 2048 columns are
+ * read once into registers, longer rows are read twice.  y may alias x.
+ * A row of -inf (or holding +inf or NaN) gives NaN, as the reference's
+ * x - max does. */
+int tt_softmax_rows_f32(const float* x, float* y, int64_t rows, int64_t cols, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,4 +1,5 @@
-"""CPU oracle for TinyTensor scaled dot-product attention (fwd, bwd, decode).
+"""CPU oracle for TinyTensor scaled dot-product attention (fwd, bwd, decode)
+and the row softmax of ``myLayer.SoftmaxForward``.
 
 TEST INFRASTRUCTURE ONLY: imported by ``tests/``, ``__graft_entry__.smoke()``
 and ``bench.py``'s ``cpu_baseline`` leg, never by the product package.
@@ -317,6 +318,32 @@ def composition_bwd_f32(q, k, v, do, scale: float, causal: bool):
     dkt = np.matmul(np.swapaxes(q, -1, -2), ds0)
     dk = np.swapaxes(dkt, -1, -2)
     return dq, dk, dv
+
+
+# ---------------------------------------------------------------------------
+# Row softmax: SoftmaxForward (Task3/Tinytensor/src/Layers.cu:324-349)
+# ---------------------------------------------------------------------------
+
+
+def softmax_rows_f64(x) -> np.ndarray:
+    """Closed form over the last axis in float64: exp(x - max) / sum exp(x - max)."""
+    x = np.asarray(x, np.float64)
+    with np.errstate(invalid="ignore", over="ignore"):
+        e = np.exp(x - np.max(x, axis=-1, keepdims=True))
+        return e / np.sum(e, axis=-1, keepdims=True)
+
+
+def softmax_rows_ref_f32(x) -> np.ndarray:
+    """The reference's GPU op order in float32 (Layers.cu:330-348): per-row max
+    (cudaChannelMax, Layers_kernels.cu:190-205), x - max (cudaChannelSub,
+    :222-235), exp (cudaChannelExp, :250-259), per-row sum (cudaChannelSum,
+    :206-221), divide (cudaChannelDiv, :236-249); also the CPU formula of
+    Softmaxloss.compute (optimizer/operators.py:611-612)."""
+    x = np.asarray(x, np.float32)
+    with np.errstate(invalid="ignore", over="ignore"):
+        m = np.max(x, axis=-1, keepdims=True)
+        e = np.exp(x - m).astype(np.float32)
+        return (e / np.sum(e, axis=-1, keepdims=True, dtype=np.float32)).astype(np.float32)
 
 
 # ---------------------------------------------------------------------------

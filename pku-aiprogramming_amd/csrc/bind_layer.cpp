@@ -1,4 +1,4 @@
-// Module `myLayer`: the attention entry points, bound in the style of
+// Module `myLayer`: the attention entry points and SoftmaxForward, bound in the style of
 // Task3/Tinytensor/src/bind_Layer.cpp:10-24 (free functions over TinyTensor
 // references), with float and bf16 overloads.
 #include <pybind11/pybind11.h>
@@ -27,4 +27,6 @@ PYBIND11_MODULE(myLayer, m) {
         py::arg("out"), py::arg("scale"));
   m.def("AttentionDecode", &AttentionDecode<bf16>, py::arg("q"), py::arg("k_cache"), py::arg("v_cache"),
         py::arg("out"), py::arg("scale"));
+  // the reference binds SoftmaxForward<float> positionally (bind_Layer.cpp:20)
+  m.def("SoftmaxForward", &SoftmaxForward<float>, py::arg("input"), py::arg("output"));
 }

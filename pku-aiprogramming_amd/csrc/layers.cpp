@@ -1,4 +1,4 @@
-// Attention layer functions: shape checks, output sizing, then one C-ABI call.
+// Attention and softmax layer functions: shape checks, output sizing, then one C-ABI call.
 #include "layers.h"
 
 #include <stdexcept>
@@ -121,6 +121,23 @@ void AttentionDecode(const TinyTensor<T>& q, const TinyTensor<T>& k_cache, const
   tt_check(tt_sync(), fn.c_str());
 }
 
+template <typename T>
+void SoftmaxForward(const TinyTensor<T>& input, TinyTensor<T>& output) {
+  static_assert(std::is_same<T, float>::value, "SoftmaxForward is float only, as in the reference");
+  const std::string fn = "SoftmaxForward";
+  need_gpu(fn, "input", input.device);
+  if (input.shape.empty()) throw std::invalid_argument(fn + ": input must have rank >= 1");
+  int64_t rows = 1;
+  for (size_t i = 0; i + 1 < input.shape.size(); ++i) rows *= input.shape[i];
+  const int64_t cols = input.shape.back();
+  if (&output != &input) {
+    if (output.device != "gpu") output.gpu();
+    output.resize(input.shape);
+  }
+  tt_check(tt_softmax_rows_f32(input.p_data, output.p_data, rows, cols, nullptr), fn.c_str());
+  tt_check(tt_sync(), fn.c_str());
+}
+
 template void AttentionForward<float>(const TinyTensor<float>&, const TinyTensor<float>&, const TinyTensor<float>&,
                                       TinyTensor<float>&, TinyTensor<float>&, float, bool);
 template void AttentionForward<bf16>(const TinyTensor<bf16>&, const TinyTensor<bf16>&, const TinyTensor<bf16>&,
@@ -135,3 +152,4 @@ template void AttentionDecode<float>(const TinyTensor<float>&, const TinyTensor<
                                      TinyTensor<float>&, float);
 template void AttentionDecode<bf16>(const TinyTensor<bf16>&, const TinyTensor<bf16>&, const TinyTensor<bf16>&,
                                     TinyTensor<bf16>&, float);
+template void SoftmaxForward<float>(const TinyTensor<float>&, TinyTensor<float>&);

@@ -1,4 +1,4 @@
-// Attention layer functions of the `myLayer` module.
+// Attention and softmax layer functions of the `myLayer` module.
 //
 // They follow the reference's layer convention (FcForward/FcBackward,
 // Task3/Tinytensor/src/Layers.h:8-26, Layers.cu:9-79): inputs are const
@@ -26,3 +26,10 @@ void AttentionBackward(const TinyTensor<T>& q, const TinyTensor<T>& k, const Tin
 template <typename T>
 void AttentionDecode(const TinyTensor<T>& q, const TinyTensor<T>& k_cache, const TinyTensor<T>& v_cache,
                      TinyTensor<T>& out, float scale);
+
+// Row softmax over the last axis (Layers.cu:324-349): output takes input's
+// shape on the "gpu" device (the reference's `output = input`, Layers.cu:333)
+// and holds exp(x - max) / sum exp(x - max) per row.  float, as the
+// reference binds it (bind_Layer.cpp:20); output may be input itself.
+template <typename T>
+void SoftmaxForward(const TinyTensor<T>& input, TinyTensor<T>& output);

@@ -1,0 +1,173 @@
+// Row softmax over the last axis of a row-major [rows, cols] fp32 matrix.
+//
+// Replaces SoftmaxForward (Task3/Tinytensor/src/Layers.cu:324-349), which
+// runs five passes -- cudaChannelMax / Sub / Exp / Sum / Div of
+// src/Layers_kernels.cu:189-257, the max and the sum each a host loop of
+// thrust calls, one per row -- with one kernel that keeps the row in
+// registers (one HBM read and one write per element) or, for long rows,
+// streams it twice.  Same arithmetic per row as the reference:
+//   m = max_c x[c];  e[c] = exp(x[c] - m);  s = sum_c e[c];  y[c] = e[c] / s
+// (the sum's association order differs: lanes, then a butterfly).
+//
+// Three shapes of work, all coalesced (lane t of a row group reads columns
+// t, t + G, t + 2G, ... for group width G):
+//   cols <= 64:   G = the next power of two >= cols lanes per row, 64 / G
+//                 rows per wave, one element per lane;
+//   cols <= 2048: one wave per row, up to 32 elements per lane in registers;
+//   longer rows:  one wave per row, pass 1 keeps a running (max, sum) per
+//                 lane, pass 2 rereads the row (from L2 for rows up to a few
+//                 hundred KB) and writes it.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+
+#include "tt_internal.h"
+
+namespace tt {
+
+namespace {
+
+constexpr int kBlock = 256;  // four waves
+
+// e^x as 2^(x log2 e) on v_exp_f32 (relative error a few 1e-7 for |x| < 10,
+// growing with |x|; the softmax outputs those terms feed are e^x / s small).
+__device__ __forceinline__ float ex(float x) { return __expf(x); }
+
+// max / sum over the G lanes of a row group (G a power of two <= 64)
+template <int G>
+__device__ __forceinline__ float group_max(float v) {
+#pragma unroll
+  for (int off = G / 2; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int off = G / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// cols <= G: one element per lane, 64 / G rows per wave.
+template <int G>
+__global__ __launch_bounds__(kBlock) void k_softmax_small(const float* __restrict__ x, float* y, int64_t rows,
+                                                         int cols) {
+  constexpr int RPB = kBlock / G;  // rows per block
+  const int t = threadIdx.x % G;
+  for (int64_t r = (int64_t)blockIdx.x * RPB + threadIdx.x / G; r < rows; r += (int64_t)gridDim.x * RPB) {
+    const bool in = t < cols;
+    const float v = in ? x[r * cols + t] : -INFINITY;
+    const float m = group_max<G>(v);
+    const float e = in ? ex(v - m) : 0.f;
+    const float s = group_sum<G>(e);
+    if (in) y[r * cols + t] = e / s;
+  }
+}
+
+// cols <= 64 * NE: one wave per row, NE elements per lane in registers.
+template <int NE>
+__global__ __launch_bounds__(kBlock) void k_softmax_reg(const float* __restrict__ x, float* y, int64_t rows,
+                                                       int cols) {
+  constexpr int WPB = kBlock / 64;
+  const int t = threadIdx.x & 63;
+  for (int64_t r = (int64_t)blockIdx.x * WPB + threadIdx.x / 64; r < rows; r += (int64_t)gridDim.x * WPB) {
+    const float* xr = x + r * cols;
+    float v[NE];
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < NE; ++i) {
+      const int c = t + 64 * i;
+      v[i] = c < cols ? xr[c] : -INFINITY;
+      m = fmaxf(m, v[i]);
+    }
+    m = group_max<64>(m);
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < NE; ++i) {
+      v[i] = t + 64 * i < cols ? ex(v[i] - m) : 0.f;
+      s += v[i];
+    }
+    s = group_sum<64>(s);
+    float* yr = y + r * cols;
+#pragma unroll
+    for (int i = 0; i < NE; ++i) {
+      const int c = t + 64 * i;
+      if (c < cols) yr[c] = v[i] / s;
+    }
+  }
+}
+
+// Any cols: one wave per row, two passes.  Pass 1: per lane a running max m
+// and a sum s of exp(x - m), rescaled when m grows; the lanes' pairs merge
+// to the row's (m, s).  Pass 2: y = exp(x - m) / s.
+__global__ __launch_bounds__(kBlock) void k_softmax_stream(const float* __restrict__ x, float* y, int64_t rows,
+                                                          int64_t cols) {
+  constexpr int WPB = kBlock / 64;
+  const int t = threadIdx.x & 63;
+  for (int64_t r = (int64_t)blockIdx.x * WPB + threadIdx.x / 64; r < rows; r += (int64_t)gridDim.x * WPB) {
+    const float* xr = x + r * cols;
+    float m = -INFINITY, s = 0.f;
+    for (int64_t c = t; c < cols; c += 64) {
+      const float v = xr[c];
+      if (v > m) {
+        s = s * ex(m - v) + 1.f;  // m = -inf: exp(-inf) = 0
+        m = v;
+      } else if (v != -INFINITY) {  // (-inf) - (-inf) would be NaN; exp(-inf - m) = 0
+        s += ex(v - m);
+      }
+    }
+    const float rm = group_max<64>(m);
+    // a lane that saw no finite value has m = -inf and s = 0 (or NaN rows
+    // propagate NaN, as the reference's x - max does)
+    s = s == 0.f ? 0.f : s * ex(m - rm);
+    s = group_sum<64>(s);
+    float* yr = y + r * cols;
+    for (int64_t c = t; c < cols; c += 64) yr[c] = ex(xr[c] - rm) / s;
+  }
+}
+
+int blocks_for(int64_t rows, int64_t rows_per_block) {
+  const int64_t b = (rows + rows_per_block - 1) / rows_per_block;
+  return (int)(b < 65536 ? b : 65536);  // grid-stride beyond this
+}
+
+}  // namespace
+
+}  // namespace tt
+
+using namespace tt;
+
+extern "C" int tt_softmax_rows_f32(const float* x, float* y, int64_t rows, int64_t cols, void* stream) {
+  if (rows < 0 || cols < 0) return fail(TT_ERR_ARG, "tt_softmax_rows_f32: negative size");
+  if (rows == 0 || cols == 0) return ok();
+  if (!x || !y) return fail(TT_ERR_ARG, "tt_softmax_rows_f32: null pointer");
+  if (cols > (int64_t(1) << 31) - 1) return fail(TT_ERR_ARG, "tt_softmax_rows_f32: row too long");
+  int rc = ensure_init();
+  if (rc) return rc;
+  hipStream_t s = stream_or_default(stream);
+  const int c = (int)cols;
+#define TT_SMALL(G)                                                                                 \
+  hipLaunchKernelGGL(k_softmax_small<G>, dim3(blocks_for(rows, kBlock / G)), dim3(kBlock), 0, s, x, y, \
+                     rows, c)
+#define TT_REG(NE) \
+  hipLaunchKernelGGL(k_softmax_reg<NE>, dim3(blocks_for(rows, kBlock / 64)), dim3(kBlock), 0, s, x, y, rows, c)
+  if (cols <= 1) TT_SMALL(1);
+  else if (cols <= 2) TT_SMALL(2);
+  else if (cols <= 4) TT_SMALL(4);
+  else if (cols <= 8) TT_SMALL(8);
+  else if (cols <= 16) TT_SMALL(16);
+  else if (cols <= 32) TT_SMALL(32);
+  else if (cols <= 64) TT_SMALL(64);
+  else if (cols <= 128) TT_REG(2);
+  else if (cols <= 256) TT_REG(4);
+  else if (cols <= 512) TT_REG(8);
+  else if (cols <= 1024) TT_REG(16);
+  else if (cols <= 2048) TT_REG(32);
+  else
+    hipLaunchKernelGGL(k_softmax_stream, dim3(blocks_for(rows, kBlock / 64)), dim3(kBlock), 0, s, x, y, rows,
+                       cols);
+#undef TT_SMALL
+#undef TT_REG
+  TT_LAUNCHED("tt_softmax_rows_f32", s);
+  return ok();
+}

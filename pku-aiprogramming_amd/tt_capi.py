@@ -55,6 +55,7 @@ _SIGS = {
     "tt_attn_bwd_bf16": (C.c_int, [_p] * 9 + [_i64] * 5 + [C.c_float, C.c_int, _p]),
     "tt_attn_decode_bf16": (C.c_int, [_p] * 5 + [_i64] * 4 + [C.c_float, _p]),
     "tt_attn_decode_f32": (C.c_int, [_p] * 5 + [_i64] * 4 + [C.c_float, _p]),
+    "tt_softmax_rows_f32": (C.c_int, [_p, _p, _i64, _i64, _p]),
 }
 
 
@@ -213,6 +214,17 @@ def attn_decode(q, k, v, o, lse, scale: float, stream=None):
     Lkv = k.shape[2]
     name = "tt_attn_decode_bf16" if q.dtype == "bf16" else "tt_attn_decode_f32"
     lib().call(name, q.ptr, k.ptr, v.ptr, o.ptr, lse.ptr if lse else None, B, H, Lkv, d, scale, stream)
+
+
+# ------------------------------------------------------------------ softmax
+
+def softmax_rows(x: DeviceBuffer, y: DeviceBuffer, stream=None):
+    """Row softmax over the last axis of x (fp32) into y (may be x)."""
+    if x.dtype != "f32" or y.dtype != "f32":
+        raise ValueError("softmax_rows: fp32 buffers only")
+    cols = x.shape[-1] if len(x.shape) else 1
+    rows = (int(np.prod(x.shape[:-1])) if len(x.shape) > 1 else 1) if cols else 0
+    lib().call("tt_softmax_rows_f32", x.ptr, y.ptr, rows, cols, stream)
 
 
 class Event:

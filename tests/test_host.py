@@ -78,6 +78,12 @@ def test_argument_errors_need_no_gpu(capi):
     assert L.lib.tt_elementwise(99, 0, None, None, None, 4, 0.0, 0.0, 0, None) == capi.TT_ERR_ARG
     assert L.lib.tt_elementwise(0, 0, None, None, None, 0, 0.0, 0.0, 0, None) == capi.TT_OK
     assert L.lib.tt_free(None) == capi.TT_OK
+    # row softmax: negative sizes, null pointers, empty work
+    sm = L.lib.tt_softmax_rows_f32
+    assert sm(None, None, -1, 4, None) == capi.TT_ERR_ARG
+    assert sm(None, None, 2, 4, None) == capi.TT_ERR_ARG and "null pointer" in L.last_error()
+    assert sm(None, None, 0, 4, None) == capi.TT_OK
+    assert sm(None, None, 3, 0, None) == capi.TT_OK
 
 
 @pytest.mark.skipif(_gpu_present(), reason="checks the no-device path")
@@ -198,6 +204,9 @@ def test_layer_functions_reject_cpu_tensors(mt):
     qb = mt.Tensor_bf16(np.zeros((1, 1, 1, 32), np.float32), "cpu")
     with pytest.raises(ValueError, match="gpu"):
         myLayer.AttentionDecode(qb, qb, qb, qb, 0.1)
+    x = mt.Tensor_float(np.zeros((4, 10), np.float32), "cpu")
+    with pytest.raises(ValueError, match="gpu"):
+        myLayer.SoftmaxForward(x, o)
 
 
 # ------------------------------------------------------------------ autograd layer

@@ -360,3 +360,60 @@ def test_planted_backward_mistakes_are_caught():
     _, tdq, tdk, _ = torch_ref(q, k, v, do, 0.5, False)
     assert orc.max_rel_err(dk_bad_transpose, tdk) > 1e-3
     assert orc.max_rel_err(dq_bad_sign, tdq) > 1e-3
+
+
+# ---------------------------------------------------------------- row softmax
+
+def _brute_softmax(x):
+    """Row by row with math.exp: the textbook definition, no max shift."""
+    out = np.empty_like(x, dtype=np.float64)
+    for idx in np.ndindex(x.shape[:-1]):
+        row = [math.exp(float(v)) for v in x[idx]]
+        s = sum(row)
+        out[idx] = [r / s for r in row]
+    return out
+
+
+def test_softmax_oracle_matches_brute_force_and_torch():
+    x = rnd((5, 3, 17), 70)
+    ref = orc.softmax_rows_f64(x)
+    assert orc.max_rel_err(ref, _brute_softmax(x)) < 1e-14
+    t = torch.softmax(torch.tensor(x, dtype=torch.float64), dim=-1).numpy()
+    assert orc.max_rel_err(ref, t) < 1e-14
+
+
+def test_softmax_oracle_closed_forms():
+    x = rnd((64, 33), 71)
+    p = orc.softmax_rows_f64(x)
+    np.testing.assert_allclose(p.sum(-1), 1.0, rtol=0, atol=1e-14)          # rows sum to one
+    np.testing.assert_allclose(orc.softmax_rows_f64(x + rnd((64, 1), 72) * 50), p, rtol=1e-12, atol=1e-15)  # shift
+    np.testing.assert_array_equal(orc.softmax_rows_f64(np.full((3, 7), 2.5)), np.full((3, 7), 1 / 7))  # constant row
+    two = rnd((100, 2), 73)
+    np.testing.assert_allclose(orc.softmax_rows_f64(two)[:, 0], 1 / (1 + np.exp(two[:, 1] - two[:, 0])), rtol=1e-13)
+    # large magnitudes: the max shift keeps it finite where the textbook form overflows
+    big = np.array([[1000.0, 999.0, -1000.0]])
+    np.testing.assert_allclose(orc.softmax_rows_f64(big)[0], [1 / (1 + math.exp(-1)), 1 / (1 + math.e), 0.0], rtol=1e-14)
+    # -inf entries get exactly 0; a row of -inf is NaN, as the reference's x - max gives
+    m = orc.softmax_rows_f64(np.array([[0.0, -np.inf, 0.0], [-np.inf, -np.inf, -np.inf]]))
+    np.testing.assert_array_equal(m[0], [0.5, 0.0, 0.5])
+    assert np.isnan(m[1]).all()
+
+
+def test_softmax_reference_order_f32_agrees_with_f64():
+    x = (rnd((300, 1000), 74) * 4).astype(np.float32)
+    ref = orc.softmax_rows_f64(x)
+    r32 = orc.softmax_rows_ref_f32(x)
+    assert r32.dtype == np.float32
+    assert orc.max_rel_err(r32, ref) < 1e-6
+
+
+def test_planted_softmax_mistakes_are_caught():
+    """Normalising over the wrong axis or dropping the max shift shows."""
+    x = rnd((8, 40), 75) * 3
+    ref = _brute_softmax(x)
+    wrong_axis = np.exp(x - x.max(0, keepdims=True)) / np.exp(x - x.max(0, keepdims=True)).sum(0, keepdims=True)
+    assert orc.max_rel_err(wrong_axis, ref) > 1e-3
+    with np.errstate(over="ignore", invalid="ignore"):
+        no_shift_big = np.exp(x * 300) / np.exp(x * 300).sum(-1, keepdims=True)  # overflows to NaN
+    assert not np.isfinite(no_shift_big).all()
+    assert np.isfinite(orc.softmax_rows_f64(x * 300)).all()
