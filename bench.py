@@ -53,6 +53,7 @@ MEASURED_TRAFFIC_MIB = {
     "attn_bwd_dkdv": 3130.6,   # includes the 2.06 GiB of dS it stores for the dQ GEMM
     "attn_bwd_dq": 2571.3,     # the dQ GEMM: reads that dS back
     "attn_decode_split": 8217.7,
+    "softmax_reg": 2048.1,     # k_softmax_reg<16>, 262144 x 1024 fp32 (profiles/softmax_rows_kernel_stats.md)
 }
 
 
@@ -172,6 +173,52 @@ def run_copy(T, steps, warmup, nbytes=1 << 30):
     return ms, 2 * nbytes / (ms * 1e-3) / 1e9
 
 
+# Row softmax (myLayer.SoftmaxForward / tt_softmax_rows_f32): HBM-bound,
+# algorithmic bytes = rows * cols * 4 read + the same written.
+SOFTMAX_CASES = [
+    dict(name="rows 262144 x 1024 (one wave per row)", rows=262144, cols=1024),
+    dict(name="rows 4096 x 65536 (16 waves per row)", rows=4096, cols=65536),
+    dict(name="rows 1024 x 262144 (two-pass stream)", rows=1024, cols=262144),
+]
+
+
+def run_softmax(T, steps, warmup, rows, cols):
+    x = T.DeviceBuffer((rows, cols), "f32")
+    y = T.DeviceBuffer((rows, cols), "f32")
+    x.fill_normal(5000, 3.0)
+    for _ in range(warmup):
+        T.softmax_rows(x, y)
+    T.lib().sync()
+    start, stop = T.Event(), T.Event()
+    start.record()
+    for _ in range(steps):
+        T.softmax_rows(x, y)
+    stop.record()
+    T.lib().sync()
+    ms = T.Event.elapsed(start, stop) / steps
+    return ms, 2 * rows * cols * 4 / (ms * 1e-3) / 1e9
+
+
+def softmax_cpu_baseline(rows=16384, cols=1024, reps=3):
+    """The reference's softmax formula (Softmaxloss.compute, optimizer/operators.py:611-612,
+    the order SoftmaxForward follows on the GPU) in float32 numpy on the host."""
+    import numpy as np
+
+    sys.path.insert(0, ROOT)
+    from oracle import attn_oracle as orc
+
+    x = np.random.default_rng(0).standard_normal((rows, cols)).astype(np.float32) * 3
+    orc.softmax_rows_ref_f32(x)
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        orc.softmax_rows_ref_f32(x)
+        ts.append(time.perf_counter() - t0)
+    t = sorted(ts)[len(ts) // 2]
+    return {"value": 2 * rows * cols * 4 / t / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"{rows} x {cols} fp32 rows, numpy max / exp / sum / divide (median of {reps}: {t * 1e3:.1f} ms)"}
+
+
 def run_gemm_ceiling(n=16384, iters=5):
     """Library bf16 GEMM (torch -> hipBLASLt), n^3, on random N(0,1) and on all-ones
     operands: the MFMA rate a tuned GEMM sustains on this box.  The instruction
@@ -249,7 +296,7 @@ def main(argv=None):
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", choices=["all", "fwdbwd", "decode", "copy", "ceiling"], default="all",
+    ap.add_argument("--only", choices=["all", "fwdbwd", "decode", "copy", "ceiling", "softmax"], default="all",
                     help="run one workload only (for profiler runs; 'copy' is the 1 GiB calibration copy, "
                          "'ceiling' the library bf16 GEMM reference)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -331,6 +378,24 @@ def main(argv=None):
             out["value"], out["unit"], out["ms_per_step"] = gbs, "GB/s", ms
             out["roofline"] = out["decode"]["roofline"]
 
+    if args.only in ("all", "softmax"):
+        cases = []
+        for c in SOFTMAX_CASES:
+            ms, gbs = run_softmax(T, args.steps, args.warmup, c["rows"], c["cols"])
+            cases.append({"workload": c["name"], "ms": ms, "value": gbs, "unit": "GB/s",
+                          "frac_of_peak": gbs / PEAK_HBM_GBS,
+                          "algorithmic_bytes_per_launch": 2 * c["rows"] * c["cols"] * 4})
+        out["softmax"] = {"cases": cases,
+                          "roofline": {"bound": "hbm", "kernel": "k_softmax_reg<16>", "achieved": cases[0]["value"],
+                                       "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                                       "frac": cases[0]["value"] / PEAK_HBM_GBS,
+                                       "traffic": traffic_bytes("softmax_reg")}}
+        if not args.no_cpu_baseline:
+            out["softmax"]["cpu_baseline"] = softmax_cpu_baseline()
+        if args.only == "softmax":
+            out["value"], out["unit"], out["ms_per_step"] = cases[0]["value"], "GB/s", cases[0]["ms"]
+            out["roofline"] = out["softmax"]["roofline"]
+
     if args.only == "all":
         # context for roofline.frac: what a tuned library GEMM sustains on real data,
         # measured in a child process (torch's HIP runtime is not the library's)
@@ -342,7 +407,7 @@ def main(argv=None):
         except (ValueError, IndexError):
             out["mfma_ceiling"] = {"error": (r.stderr or "no output").strip().splitlines()[-1:]}
 
-    if not args.no_cpu_baseline and args.cpu_heads > 0:
+    if not args.no_cpu_baseline and args.cpu_heads > 0 and args.only in ("all", "fwdbwd"):
         out["cpu_baseline"] = cpu_baseline(args.cpu_heads)
 
     print(json.dumps(out), flush=True)

@@ -14,9 +14,10 @@
 //   cols <= 64:   G = the next power of two >= cols lanes per row, 64 / G
 //                 rows per wave, one element per lane;
 //   cols <= 2048: one wave per row, up to 32 elements per lane in registers;
-//   longer rows:  one wave per row, pass 1 keeps a running (max, sum) per
-//                 lane, pass 2 rereads the row (from L2 for rows up to a few
-//                 hundred KB) and writes it.
+//   cols <= 65536: one workgroup of 4 or 16 waves per row, up to 64
+//                 elements per lane in registers, partials through LDS;
+//   longer rows:  one workgroup of 16 waves per row; pass 1 keeps a running
+//                 (max, sum) per lane, pass 2 rereads the row and writes it.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -97,32 +98,115 @@ __global__ __launch_bounds__(kBlock) void k_softmax_reg(const float* __restrict_
   }
 }
 
-// Any cols: one wave per row, two passes.  Pass 1: per lane a running max m
-// and a sum s of exp(x - m), rescaled when m grows; the lanes' pairs merge
-// to the row's (m, s).  Pass 2: y = exp(x - m) / s.
-__global__ __launch_bounds__(kBlock) void k_softmax_stream(const float* __restrict__ x, float* y, int64_t rows,
-                                                          int64_t cols) {
-  constexpr int WPB = kBlock / 64;
-  const int t = threadIdx.x & 63;
-  for (int64_t r = (int64_t)blockIdx.x * WPB + threadIdx.x / 64; r < rows; r += (int64_t)gridDim.x * WPB) {
+// cols <= 64 W NE: one workgroup of W waves per row, NE elements per lane in
+// registers; the waves' partial max / sum meet in LDS.
+template <int NE, int W>
+__global__ __launch_bounds__(64 * W) void k_softmax_block(const float* __restrict__ x, float* y, int64_t rows,
+                                                         int cols) {
+  __shared__ float red_m[W], red_s[W];
+  const int t = threadIdx.x, w = t >> 6;
+  for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {  // uniform per workgroup
     const float* xr = x + r * cols;
-    float m = -INFINITY, s = 0.f;
-    for (int64_t c = t; c < cols; c += 64) {
-      const float v = xr[c];
-      if (v > m) {
-        s = s * ex(m - v) + 1.f;  // m = -inf: exp(-inf) = 0
-        m = v;
-      } else if (v != -INFINITY) {  // (-inf) - (-inf) would be NaN; exp(-inf - m) = 0
-        s += ex(v - m);
+    float v[NE];
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < NE; ++i) {
+      const int c = t + 64 * W * i;
+      v[i] = c < cols ? xr[c] : -INFINITY;
+      m = fmaxf(m, v[i]);
+    }
+    m = group_max<64>(m);
+    if ((t & 63) == 0) red_m[w] = m;
+    __syncthreads();
+    m = red_m[0];
+#pragma unroll
+    for (int k = 1; k < W; ++k) m = fmaxf(m, red_m[k]);
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < NE; ++i) {
+      v[i] = t + 64 * W * i < cols ? ex(v[i] - m) : 0.f;
+      s += v[i];
+    }
+    s = group_sum<64>(s);
+    if ((t & 63) == 0) red_s[w] = s;
+    __syncthreads();
+    s = red_s[0];
+#pragma unroll
+    for (int k = 1; k < W; ++k) s += red_s[k];
+    float* yr = y + r * cols;
+#pragma unroll
+    for (int i = 0; i < NE; ++i) {
+      const int c = t + 64 * W * i;
+      if (c < cols) yr[c] = v[i] / s;
+    }
+    __syncthreads();  // red_m / red_s are reused by the next row
+  }
+}
+
+// Any cols: one workgroup of W waves per row, two passes, four loads in
+// flight per lane.  Pass 1: per lane a running max m and a (compensated) sum
+// s of exp(x - m), rescaled when m grows; lanes, then waves (through LDS),
+// merge their pairs to the row's (m, s).  Pass 2: y = exp(x - m) / s.
+template <int W>
+__global__ __launch_bounds__(64 * W) void k_softmax_stream(const float* __restrict__ x, float* y, int64_t rows,
+                                                          int64_t cols) {
+  constexpr int U = 4, STEP = 64 * W * U;
+  __shared__ float red_m[W], red_s[W];
+  const int t = threadIdx.x, w = t >> 6;
+  for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {  // uniform per workgroup
+    const float* xr = x + r * cols;
+    // s carries a Kahan compensation e: a lane adds cols / (64 W) terms in
+    // sequence, which in plain fp32 would cost about that many roundings
+    float m = -INFINITY, s = 0.f, e = 0.f;
+    auto add = [&](float a) {
+      const float yv = a - e, tv = s + yv;
+      e = (tv - s) - yv;
+      s = tv;
+    };
+    for (int64_t c0 = t; c0 < cols; c0 += STEP) {
+      float v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) v[u] = c0 + 64 * W * u < cols ? xr[c0 + 64 * W * u] : -INFINITY;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (v[u] > m) {
+          const float f = ex(m - v[u]);  // m = -inf: exp(-inf) = 0
+          s *= f;
+          e *= f;
+          add(1.f);
+          m = v[u];
+        } else if (v[u] != -INFINITY) {  // (-inf) - (-inf) would be NaN; exp(-inf - m) = 0
+          add(ex(v[u] - m));
+        }
       }
     }
-    const float rm = group_max<64>(m);
-    // a lane that saw no finite value has m = -inf and s = 0 (or NaN rows
-    // propagate NaN, as the reference's x - max does)
-    s = s == 0.f ? 0.f : s * ex(m - rm);
-    s = group_sum<64>(s);
+    s -= e;
+    // merge (m, s) pairs: a pair that saw no finite value has m = -inf and
+    // s = 0 and adds nothing (NaN rows propagate NaN, as the reference's
+    // x - max does)
+    float rm = group_max<64>(m);
+    s = group_sum<64>(s == 0.f ? 0.f : s * ex(m - rm));
+    if ((t & 63) == 0) {
+      red_m[w] = rm;
+      red_s[w] = s;
+    }
+    __syncthreads();
+    float bm = red_m[0];
+#pragma unroll
+    for (int k = 1; k < W; ++k) bm = fmaxf(bm, red_m[k]);
+    float bs = 0.f;
+#pragma unroll
+    for (int k = 0; k < W; ++k) bs += red_s[k] == 0.f ? 0.f : red_s[k] * ex(red_m[k] - bm);
     float* yr = y + r * cols;
-    for (int64_t c = t; c < cols; c += 64) yr[c] = ex(xr[c] - rm) / s;
+    for (int64_t c0 = t; c0 < cols; c0 += STEP) {
+      float v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) v[u] = c0 + 64 * W * u < cols ? xr[c0 + 64 * W * u] : 0.f;
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (c0 + 64 * W * u < cols) yr[c0 + 64 * W * u] = ex(v[u] - bm) / bs;
+    }
+    __syncthreads();  // red_m / red_s are reused by the next row
   }
 }
 
@@ -151,6 +235,8 @@ extern "C" int tt_softmax_rows_f32(const float* x, float* y, int64_t rows, int64
                      rows, c)
 #define TT_REG(NE) \
   hipLaunchKernelGGL(k_softmax_reg<NE>, dim3(blocks_for(rows, kBlock / 64)), dim3(kBlock), 0, s, x, y, rows, c)
+#define TT_BLOCK(NE, W) \
+  hipLaunchKernelGGL((k_softmax_block<NE, W>), dim3(blocks_for(rows, 1)), dim3(64 * W), 0, s, x, y, rows, c)
   if (cols <= 1) TT_SMALL(1);
   else if (cols <= 2) TT_SMALL(2);
   else if (cols <= 4) TT_SMALL(4);
@@ -163,11 +249,16 @@ extern "C" int tt_softmax_rows_f32(const float* x, float* y, int64_t rows, int64
   else if (cols <= 512) TT_REG(8);
   else if (cols <= 1024) TT_REG(16);
   else if (cols <= 2048) TT_REG(32);
+  else if (cols <= 4096) TT_BLOCK(16, 4);
+  else if (cols <= 8192) TT_BLOCK(32, 4);
+  else if (cols <= 16384) TT_BLOCK(16, 16);
+  else if (cols <= 32768) TT_BLOCK(32, 16);
+  else if (cols <= 65536) TT_BLOCK(64, 16);
   else
-    hipLaunchKernelGGL(k_softmax_stream, dim3(blocks_for(rows, kBlock / 64)), dim3(kBlock), 0, s, x, y, rows,
-                       cols);
+    hipLaunchKernelGGL(k_softmax_stream<16>, dim3(blocks_for(rows, 1)), dim3(1024), 0, s, x, y, rows, cols);
 #undef TT_SMALL
 #undef TT_REG
+#undef TT_BLOCK
   TT_LAUNCHED("tt_softmax_rows_f32", s);
   return ok();
 }

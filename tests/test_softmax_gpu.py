@@ -51,9 +51,11 @@ def _check(name, y, x):
 
 
 # every kernel shape: lane groups of 1..64, one wave with 2..32 elements per
-# lane, and the two-pass stream, at the edges of each
+# lane, workgroups of 4 / 16 waves with 16..64 elements per lane, and the
+# two-pass stream, at the edges of each
 COLS = [1, 2, 3, 5, 8, 10, 16, 17, 31, 32, 33, 63, 64, 65, 100, 128, 129, 255, 256, 257, 500, 512, 513, 1000,
-        1024, 1025, 2047, 2048, 2049, 4096, 10000, 65537]
+        1024, 1025, 2047, 2048, 2049, 4095, 4096, 4097, 8192, 8193, 10000, 16384, 16385, 32768, 32769, 65535,
+        65536, 65537, 200000]
 
 
 @pytest.mark.parametrize("cols", COLS)
@@ -64,21 +66,23 @@ def test_rows_of_every_length(capi, cols):
     _check(f"[{rows}, {cols}]", _softmax_gpu(capi, x), x)
 
 
-@pytest.mark.parametrize("cols", [10, 100, 1000, 3000])
+@pytest.mark.parametrize("cols", [10, 100, 1000, 3000, 40000, 70000])
 def test_in_place(capi, cols):
     _say(f"softmax in place cols={cols}")
     x = np.random.default_rng(7 + cols).standard_normal((33, cols)).astype(np.float32)
     _check("in place", _softmax_gpu(capi, x, inplace=True), x)
 
 
-def test_many_rows_grid_stride(capi):
-    # more rows than the launch's 65536 blocks cover at once (4 rows per block)
-    x = np.random.default_rng(11).standard_normal((300_000, 70)).astype(np.float32)
-    _say("softmax rows=300000 cols=70 (grid-stride)")
-    _check("[300000, 70]", _softmax_gpu(capi, x), x)
+@pytest.mark.parametrize("rows,cols", [(300_000, 70), (65_600, 2100)])
+def test_many_rows_grid_stride(capi, rows, cols):
+    # more rows than the launch's 65536 workgroups cover at once (4 rows per
+    # workgroup for one wave per row; one row per workgroup of 4 waves)
+    x = np.random.default_rng(11).standard_normal((rows, cols)).astype(np.float32)
+    _say(f"softmax rows={rows} cols={cols} (grid-stride)")
+    _check(f"[{rows}, {cols}]", _softmax_gpu(capi, x), x)
 
 
-@pytest.mark.parametrize("cols", [7, 300, 5000])
+@pytest.mark.parametrize("cols", [7, 300, 5000, 70000])
 def test_large_magnitudes_and_infinities(capi, cols):
     _say(f"softmax extremes cols={cols}")
     rng = np.random.default_rng(20 + cols)
