@@ -185,6 +185,21 @@ int tt_attn_decode_f32(const float* q, const float* k, const float* v, float* o,
  * x - max does. */
 int tt_softmax_rows_f32(const float* x, float* y, int64_t rows, int64_t cols, void* stream);
 
+/* ---------------------------------------------------------------- GEMM */
+
+/* C = alpha op(A) op(B) + beta C, all row-major: op(A) is m x k, op(B) is
+ * k x n, C is m x n (ldc = n).  transa = 0: A stored m x k (lda = k); 1: A
+ * stored k x m (lda = m).  transb = 0: B stored k x n (ldb = n); 1: B stored
+ * n x k (ldb = k).  beta = 0 does not read C.  Replaces cudaGemm
+ * (src/Layers_kernels.cu:10-30: a cuBLAS handle created and destroyed around
+ * one cublasSgemm per call), called by FcForward / FcBackward (src/Layers.cu:
+ * 26-77) and ConvForward / ConvBackward (:197, :247-248).  fp32: fp32
+ * products and sums on the fp32 MFMA; bf16: bf16 A, B, C with fp32 sums. */
+int tt_gemm_f32(int transa, int transb, int64_t m, int64_t n, int64_t k, float alpha,
+                const float* A, const float* B, float beta, float* C, void* stream);
+int tt_gemm_bf16(int transa, int transb, int64_t m, int64_t n, int64_t k, float alpha,
+                 const uint16_t* A, const uint16_t* B, float beta, uint16_t* C, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

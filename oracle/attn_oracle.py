@@ -1,5 +1,5 @@
-"""CPU oracle for TinyTensor scaled dot-product attention (fwd, bwd, decode)
-and the row softmax of ``myLayer.SoftmaxForward``.
+"""CPU oracle for TinyTensor scaled dot-product attention (fwd, bwd, decode),
+the row softmax of ``myLayer.SoftmaxForward`` and the ``cudaGemm`` contract.
 
 TEST INFRASTRUCTURE ONLY: imported by ``tests/``, ``__graft_entry__.smoke()``
 and ``bench.py``'s ``cpu_baseline`` leg, never by the product package.
@@ -344,6 +344,27 @@ def softmax_rows_ref_f32(x) -> np.ndarray:
         m = np.max(x, axis=-1, keepdims=True)
         e = np.exp(x - m).astype(np.float32)
         return (e / np.sum(e, axis=-1, keepdims=True, dtype=np.float32)).astype(np.float32)
+
+
+# ---------------------------------------------------------------------------
+# GEMM: the cudaGemm contract (Task3/Tinytensor/src/Layers_kernels.cu:10-30)
+# ---------------------------------------------------------------------------
+
+
+def gemm_f64(transa: bool, transb: bool, alpha: float, A, B, beta: float, C=None) -> np.ndarray:
+    """alpha op(A) @ op(B) + beta C in float64, row-major.  op(A) = A.T when
+    transa (A stored k x m), op(B) = B.T when transb (B stored n x k); the
+    reference reaches the same product by calling cublasSgemm on the
+    column-major views with the operands swapped (Layers_kernels.cu:22-27).
+    beta = 0 ignores C (it may hold anything)."""
+    a = np.asarray(A, np.float64)
+    b = np.asarray(B, np.float64)
+    a = a.T if transa else a
+    b = b.T if transb else b
+    out = alpha * (a @ b)
+    if beta != 0.0:
+        out = out + beta * np.asarray(C, np.float64)
+    return out
 
 
 # ---------------------------------------------------------------------------

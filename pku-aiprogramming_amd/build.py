@@ -29,7 +29,7 @@ CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 INCLUDE = os.path.join(ROOT, "include")
 
-HIP_SOURCES = ["tt_runtime.hip", "attn_fwd.hip", "attn_bwd.hip", "attn_decode.hip", "softmax.hip"]
+HIP_SOURCES = ["tt_runtime.hip", "attn_fwd.hip", "attn_bwd.hip", "attn_decode.hip", "softmax.hip", "gemm.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 # Packed-FP32 instructions are kept out of every kernel; the host pass warns
 # that it does not know the feature, which is harmless.

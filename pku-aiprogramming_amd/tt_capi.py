@@ -56,6 +56,8 @@ _SIGS = {
     "tt_attn_decode_bf16": (C.c_int, [_p] * 5 + [_i64] * 4 + [C.c_float, _p]),
     "tt_attn_decode_f32": (C.c_int, [_p] * 5 + [_i64] * 4 + [C.c_float, _p]),
     "tt_softmax_rows_f32": (C.c_int, [_p, _p, _i64, _i64, _p]),
+    "tt_gemm_f32": (C.c_int, [C.c_int, C.c_int, _i64, _i64, _i64, C.c_float, _p, _p, C.c_float, _p, _p]),
+    "tt_gemm_bf16": (C.c_int, [C.c_int, C.c_int, _i64, _i64, _i64, C.c_float, _p, _p, C.c_float, _p, _p]),
 }
 
 
@@ -214,6 +216,17 @@ def attn_decode(q, k, v, o, lse, scale: float, stream=None):
     Lkv = k.shape[2]
     name = "tt_attn_decode_bf16" if q.dtype == "bf16" else "tt_attn_decode_f32"
     lib().call(name, q.ptr, k.ptr, v.ptr, o.ptr, lse.ptr if lse else None, B, H, Lkv, d, scale, stream)
+
+
+# ------------------------------------------------------------------ GEMM
+
+def gemm(transa: bool, transb: bool, m: int, n: int, k: int, alpha: float, A: DeviceBuffer, B: DeviceBuffer,
+         beta: float, C: DeviceBuffer, stream=None):
+    """C = alpha op(A) op(B) + beta C (row-major, the cudaGemm contract)."""
+    if not (A.dtype == B.dtype == C.dtype):
+        raise ValueError("gemm: A, B and C must share one dtype")
+    name = "tt_gemm_bf16" if C.dtype == "bf16" else "tt_gemm_f32"
+    lib().call(name, int(transa), int(transb), m, n, k, alpha, A.ptr, B.ptr, beta, C.ptr, stream)
 
 
 # ------------------------------------------------------------------ softmax

@@ -417,3 +417,57 @@ def test_planted_softmax_mistakes_are_caught():
         no_shift_big = np.exp(x * 300) / np.exp(x * 300).sum(-1, keepdims=True)  # overflows to NaN
     assert not np.isfinite(no_shift_big).all()
     assert np.isfinite(orc.softmax_rows_f64(x * 300)).all()
+
+
+# ---------------------------------------------------------------- GEMM (cudaGemm contract)
+
+def _brute_gemm(ta, tb, alpha, A, B, beta, C):
+    """Element by element from the contract's index formulas (row-major, lda = k or m, ldb = n or k)."""
+    m = A.shape[1] if ta else A.shape[0]
+    k = A.shape[0] if ta else A.shape[1]
+    n = B.shape[0] if tb else B.shape[1]
+    out = np.zeros((m, n))
+    for i in range(m):
+        for j in range(n):
+            acc = 0.0
+            for p in range(k):
+                a = A[p, i] if ta else A[i, p]
+                b = B[j, p] if tb else B[p, j]
+                acc += a * b
+            out[i, j] = alpha * acc + (beta * C[i, j] if beta != 0 else 0.0)
+    return out
+
+
+@pytest.mark.parametrize("ta", [False, True])
+@pytest.mark.parametrize("tb", [False, True])
+def test_gemm_oracle_matches_brute_force(ta, tb):
+    m, n, k = 5, 7, 3
+    A = rnd((k, m) if ta else (m, k), 80)
+    B = rnd((n, k) if tb else (k, n), 81)
+    C = rnd((m, n), 82)
+    for alpha, beta in [(1.0, 0.0), (0.5, 2.0), (-1.25, 1.0)]:
+        np.testing.assert_allclose(orc.gemm_f64(ta, tb, alpha, A, B, beta, C),
+                                   _brute_gemm(ta, tb, alpha, A, B, beta, C), rtol=1e-14, atol=1e-14)
+
+
+def test_gemm_oracle_identities():
+    A, B = rnd((40, 30), 83), rnd((30, 20), 84)
+    ab = orc.gemm_f64(False, False, 1.0, A, B, 0.0)
+    np.testing.assert_allclose(ab, (torch.tensor(A) @ torch.tensor(B)).numpy(), rtol=1e-13)
+    # (A B)^T = B^T A^T through the transpose flags on the stored matrices
+    np.testing.assert_allclose(orc.gemm_f64(True, True, 1.0, B, A, 0.0), ab.T, rtol=1e-13)
+    # identity, linearity in alpha, beta = 0 ignores a NaN C
+    np.testing.assert_allclose(orc.gemm_f64(False, False, 1.0, A, np.eye(30), 0.0), A, rtol=0, atol=0)
+    np.testing.assert_allclose(orc.gemm_f64(False, False, 3.0, A, B, 0.0), 3 * ab, rtol=1e-14)
+    assert np.isfinite(orc.gemm_f64(False, False, 1.0, A, B, 0.0, np.full((40, 20), np.nan))).all()
+    # k = 0: only beta C remains
+    C = rnd((4, 6), 85)
+    np.testing.assert_allclose(orc.gemm_f64(False, False, 1.0, np.zeros((4, 0)), np.zeros((0, 6)), 2.0, C), 2 * C)
+
+
+def test_planted_gemm_mistakes_are_caught():
+    """Ignoring a transpose flag or swapping the operands shows."""
+    A, B = rnd((6, 6), 86), rnd((6, 6), 87)
+    good = _brute_gemm(True, False, 1.0, A, B, 0.0, None)
+    assert orc.max_rel_err(orc.gemm_f64(False, False, 1.0, A, B, 0.0), good) > 1e-3
+    assert orc.max_rel_err(orc.gemm_f64(True, False, 1.0, B, A, 0.0), good) > 1e-3
