@@ -199,6 +199,35 @@ def run_softmax(T, steps, warmup, rows, cols):
     return ms, 2 * rows * cols * 4 / (ms * 1e-3) / 1e9
 
 
+# GEMM (tt_gemm_f32 / tt_gemm_bf16, the cudaGemm contract): MFMA-bound,
+# 2 m n k FLOP per call.
+GEMM_CASES = [
+    dict(dtype="f32", m=4096, n=4096, k=4096, ta=False, tb=False),
+    dict(dtype="bf16", m=8192, n=8192, k=8192, ta=False, tb=False),
+    dict(dtype="bf16", m=8192, n=8192, k=8192, ta=True, tb=True),
+]
+PEAK_FP32_MFMA_TFLOPS = 157.3
+
+
+def run_gemm(T, steps, warmup, dtype, m, n, k, ta, tb):
+    A = T.DeviceBuffer((k, m) if ta else (m, k), dtype)
+    B = T.DeviceBuffer((n, k) if tb else (k, n), dtype)
+    Cb = T.DeviceBuffer((m, n), dtype)
+    A.fill_normal(6000)
+    B.fill_normal(6001)
+    for _ in range(warmup):
+        T.gemm(ta, tb, m, n, k, 1.0, A, B, 0.0, Cb)
+    T.lib().sync()
+    start, stop = T.Event(), T.Event()
+    start.record()
+    for _ in range(steps):
+        T.gemm(ta, tb, m, n, k, 1.0, A, B, 0.0, Cb)
+    stop.record()
+    T.lib().sync()
+    ms = T.Event.elapsed(start, stop) / steps
+    return ms, 2.0 * m * n * k / (ms * 1e-3) / 1e12
+
+
 def softmax_cpu_baseline(rows=16384, cols=1024, reps=3):
     """The reference's softmax formula (Softmaxloss.compute, optimizer/operators.py:611-612,
     the order SoftmaxForward follows on the GPU) in float32 numpy on the host."""
@@ -296,7 +325,7 @@ def main(argv=None):
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", choices=["all", "fwdbwd", "decode", "copy", "ceiling", "softmax"], default="all",
+    ap.add_argument("--only", choices=["all", "fwdbwd", "decode", "copy", "ceiling", "softmax", "gemm"], default="all",
                     help="run one workload only (for profiler runs; 'copy' is the 1 GiB calibration copy, "
                          "'ceiling' the library bf16 GEMM reference)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -395,6 +424,17 @@ def main(argv=None):
         if args.only == "softmax":
             out["value"], out["unit"], out["ms_per_step"] = cases[0]["value"], "GB/s", cases[0]["ms"]
             out["roofline"] = out["softmax"]["roofline"]
+
+    if args.only in ("all", "gemm"):
+        cases = []
+        for c in GEMM_CASES:
+            ms, tf = run_gemm(T, max(3, args.steps // 4), 2, **c)
+            peak = PEAK_BF16_TFLOPS if c["dtype"] == "bf16" else PEAK_FP32_MFMA_TFLOPS
+            cases.append({"workload": f"{c['dtype']} {c['m']}x{c['n']}x{c['k']} ta={int(c['ta'])} tb={int(c['tb'])}",
+                          "ms": ms, "value": tf, "unit": "TFLOP/s", "frac_of_peak": tf / peak, "peak": peak})
+        out["gemm"] = {"cases": cases}
+        if args.only == "gemm":
+            out["value"], out["unit"], out["ms_per_step"] = cases[1]["value"], "TFLOP/s", cases[1]["ms"]
 
     if args.only == "all":
         # context for roofline.frac: what a tuned library GEMM sustains on real data,
