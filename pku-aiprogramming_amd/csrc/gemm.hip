@@ -11,8 +11,9 @@
 // beta = 0 does not read C.  fp32 on v_mfma_f32_32x32x2f32 (fp32 products,
 // fp32 sums) and bf16 on v_mfma_f32_32x32x16_bf16 (fp32 sums, bf16 C).
 //
-// Workgroup = 4 waves, a 128 x 128 tile of C (each wave 64 x 64: 2 x 2
-// MFMA blocks of 32 x 32); k in steps of BK through a two-stage LDS ring,
+// Workgroup = 4 waves, a 128 x 128 (fp32) or 128 x 256 (bf16) tile of C
+// (each wave 64 x 64 or 64 x 128: 2 x 2 or 2 x 4 MFMA blocks of 32 x 32);
+// k in steps of BK through a two-stage LDS ring,
 // global -> registers -> LDS, one barrier per step.  Each operand tile keeps
 // its stored layout in LDS (rows padded against bank conflicts):
 //   k contiguous in memory (A as stored with transa = 0, B with transb = 1):
@@ -33,12 +34,17 @@ namespace tt {
 
 namespace {
 
-constexpr int GM = 128, GN = 128;  // C tile per workgroup
+constexpr int GM = 128;  // C tile rows per workgroup
+
+#ifndef TT_GEMM_WIDE
+#define TT_GEMM_WIDE 1
+#endif
 
 template <typename T>
 struct GemmT;
 template <>
 struct GemmT<float> {
+  static constexpr int GN = 128;          // C tile columns per workgroup
   static constexpr int BK = 16, EPC = 4;  // k per step; elements per 16-byte chunk
   static constexpr int PAD_K = 4;         // [rows][BK + PAD_K]: 80-byte rows keep 16-byte stores aligned
   static constexpr int PAD_R = 4;         // [BK][rows + PAD_R]
@@ -47,7 +53,10 @@ struct GemmT<float> {
 };
 template <>
 struct GemmT<u16> {
-  static constexpr int BK = 64, EPC = 8;
+  // 128 x 256 tiles (each wave 64 x 128) halve the operand traffic per MFMA
+  // of 128 x 128 ones; BK = 32 keeps two workgroups' rings in LDS
+  static constexpr int GN = TT_GEMM_WIDE ? 256 : 128;
+  static constexpr int BK = TT_GEMM_WIDE ? 32 : 64, EPC = 8;
   static constexpr int PAD_K = 8;   // row stride 144 B: 16 lanes of 16-byte row reads hit disjoint banks
   static constexpr int PAD_R = 16;  // row stride 288 B: the 4 rows of a transpose read hit disjoint banks
   static __device__ __forceinline__ float to_f(u16 x) { return bf16_to_f32(x); }
@@ -144,6 +153,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(int M, int N, int K, float alph
                                                 int64_t lda, const T* __restrict__ B, int64_t ldb, float beta,
                                                 T* C) {
   using G = GemmT<T>;
+  constexpr int GN = G::GN, NB = GN / 64;  // MFMA blocks per wave along n
   constexpr int BK = G::BK, KS = sizeof(T) == 2 ? BK / 16 : BK / 2;  // MFMA k-steps per BK
   using TileA = OpTile<T, GM, !TA>;  // A as stored with transa = 0 is [m][k]: k contiguous
   using TileB = OpTile<T, GN, TB>;   // B as stored with transb = 1 is [n][k]: k contiguous
@@ -152,13 +162,13 @@ __global__ __launch_bounds__(256, 2) void k_gemm(int M, int N, int K, float alph
 
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
   const int m0 = blockIdx.y * GM, n0 = blockIdx.x * GN;
-  const int wm = 64 * (w >> 1), wn = 64 * (w & 1);  // this wave's 64 x 64 of the tile
+  const int wm = 64 * (w >> 1), wn = (GN / 2) * (w & 1);  // this wave's 64 x GN/2 of the tile
 
-  f32x16 acc[2][2];
+  f32x16 acc[2][NB];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
+    for (int j = 0; j < NB; ++j) acc[i][j] = f32x16{};
 
   TileA ta;
   TileB tb;
@@ -180,18 +190,16 @@ __global__ __launch_bounds__(256, 2) void k_gemm(int M, int N, int K, float alph
     for (int ks = 0; ks < KS; ++ks) {
       const auto a0 = operand<T, GM, !TA>(sA[cur], wm, ks);
       const auto a1 = operand<T, GM, !TA>(sA[cur], wm + 32, ks);
-      const auto b0 = operand<T, GN, TB>(sB[cur], wn, ks);
-      const auto b1 = operand<T, GN, TB>(sB[cur], wn + 32, ks);
-      if constexpr (sizeof(T) == 2) {
-        acc[0][0] = mfma_bf16_32x32x16(a0, b0, acc[0][0]);
-        acc[0][1] = mfma_bf16_32x32x16(a0, b1, acc[0][1]);
-        acc[1][0] = mfma_bf16_32x32x16(a1, b0, acc[1][0]);
-        acc[1][1] = mfma_bf16_32x32x16(a1, b1, acc[1][1]);
-      } else {
-        acc[0][0] = mfma_f32_32x32x2(a0, b0, acc[0][0]);
-        acc[0][1] = mfma_f32_32x32x2(a0, b1, acc[0][1]);
-        acc[1][0] = mfma_f32_32x32x2(a1, b0, acc[1][0]);
-        acc[1][1] = mfma_f32_32x32x2(a1, b1, acc[1][1]);
+#pragma unroll
+      for (int j = 0; j < NB; ++j) {
+        const auto b = operand<T, GN, TB>(sB[cur], wn + 32 * j, ks);
+        if constexpr (sizeof(T) == 2) {
+          acc[0][j] = mfma_bf16_32x32x16(a0, b, acc[0][j]);
+          acc[1][j] = mfma_bf16_32x32x16(a1, b, acc[1][j]);
+        } else {
+          acc[0][j] = mfma_f32_32x32x2(a0, b, acc[0][j]);
+          acc[1][j] = mfma_f32_32x32x2(a1, b, acc[1][j]);
+        }
       }
     }
     if (kt + 1 < nk) {
@@ -206,7 +214,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(int M, int N, int K, float alph
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < NB; ++j) {
       const int n = n0 + wn + 32 * j + (l & 31);
       if (n >= N) continue;
 #pragma unroll
@@ -231,6 +239,7 @@ int gemm_launch(const char* fn, int transa, int transb, int64_t m, int64_t n, in
     return fail(TT_ERR_ARG, std::string(fn) + ": dimension above 2^31 - 1");
   if (m == 0 || n == 0) return ok();
   if (!C || (k > 0 && (!A || !B))) return fail(TT_ERR_ARG, std::string(fn) + ": null pointer");
+  constexpr int GN = GemmT<T>::GN;
   const int64_t gx = (n + GN - 1) / GN, gy = (m + GM - 1) / GM;
   if (gy > 65535) return fail(TT_ERR_ARG, std::string(fn) + ": m too large");
   int rc = ensure_init();
