@@ -228,6 +228,54 @@ def run_gemm(T, steps, warmup, dtype, m, n, k, ta, tb):
     return ms, 2.0 * m * n * k / (ms * 1e-3) / 1e12
 
 
+# Host <-> device transfers (tt_memcpy_h2d / tt_memcpy_d2h and the converting
+# bf16 copies): bound by the host link; the ceiling is the DMA rate from
+# pinned host memory, measured beside them.
+IO_BYTES = 512 << 20
+
+
+def run_io(T, reps=4):
+    import ctypes as C
+
+    import numpy as np
+
+    L = T.lib()
+    n = IO_BYTES // 4
+    x = np.random.default_rng(0).standard_normal(n, dtype=np.float32)
+    out = np.empty_like(x)
+    d = T.DeviceBuffer((n,), "f32")
+    db = T.DeviceBuffer((n,), "bf16")
+    pin = C.c_void_p()
+    L.call("tt_host_malloc", C.byref(pin), IO_BYTES)
+    try:
+        legs = [
+            ("h2d f32, pageable numpy source (staged)", lambda: L.call("tt_memcpy_h2d", d.ptr, x.ctypes.data, IO_BYTES)),
+            ("d2h f32, pageable numpy destination (staged)",
+             lambda: L.call("tt_memcpy_d2h", out.ctypes.data, d.ptr, IO_BYTES)),
+            ("h2d fp32 -> bf16 (converted in the staging pass)",
+             lambda: L.call("tt_upload_bf16_from_f32", db.ptr, x.ctypes.data, n)),
+            ("d2h bf16 -> fp32 (converted in the staging pass)",
+             lambda: L.call("tt_download_bf16_to_f32", out.ctypes.data, db.ptr, n)),
+            ("h2d f32, pinned source (direct DMA: ceiling)", lambda: L.call("tt_memcpy_h2d", d.ptr, pin.value, IO_BYTES)),
+            ("d2h f32, pinned destination (direct DMA: ceiling)",
+             lambda: L.call("tt_memcpy_d2h", pin.value, d.ptr, IO_BYTES)),
+        ]
+        cases = []
+        for name, fn in legs:
+            fn()
+            ts = []
+            for _ in range(reps):
+                t0 = time.perf_counter()
+                fn()
+                ts.append(time.perf_counter() - t0)
+            t = min(ts)
+            cases.append({"workload": name, "ms": t * 1e3, "value": IO_BYTES / t / 1e9,
+                          "unit": "GB/s (of fp32 host bytes)"})
+    finally:
+        L.call("tt_host_free", pin.value)
+    return cases
+
+
 def softmax_cpu_baseline(rows=16384, cols=1024, reps=3):
     """The reference's softmax formula (Softmaxloss.compute, optimizer/operators.py:611-612,
     the order SoftmaxForward follows on the GPU) in float32 numpy on the host."""
@@ -325,7 +373,7 @@ def main(argv=None):
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", choices=["all", "fwdbwd", "decode", "copy", "ceiling", "softmax", "gemm"], default="all",
+    ap.add_argument("--only", choices=["all", "fwdbwd", "decode", "copy", "ceiling", "softmax", "gemm", "io"], default="all",
                     help="run one workload only (for profiler runs; 'copy' is the 1 GiB calibration copy, "
                          "'ceiling' the library bf16 GEMM reference)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -404,6 +452,8 @@ def main(argv=None):
                          "algorithmic_bytes_per_launch": split_bytes},
         }
         if args.only == "decode":
+            out["metric"], out["dtype"] = "attn decode KV-read HBM GB/s", "bf16"
+            out["config"] = {"workload": out["decode"]["workload"], **C4}
             out["value"], out["unit"], out["ms_per_step"] = gbs, "GB/s", ms
             out["roofline"] = out["decode"]["roofline"]
 
@@ -422,6 +472,8 @@ def main(argv=None):
         if not args.no_cpu_baseline:
             out["softmax"]["cpu_baseline"] = softmax_cpu_baseline()
         if args.only == "softmax":
+            out["metric"], out["dtype"] = "row softmax HBM GB/s (read + write)", "f32"
+            out["config"] = {"workload": cases[0]["workload"]}
             out["value"], out["unit"], out["ms_per_step"] = cases[0]["value"], "GB/s", cases[0]["ms"]
             out["roofline"] = out["softmax"]["roofline"]
 
@@ -434,7 +486,21 @@ def main(argv=None):
                           "ms": ms, "value": tf, "unit": "TFLOP/s", "frac_of_peak": tf / peak, "peak": peak})
         out["gemm"] = {"cases": cases}
         if args.only == "gemm":
+            out["metric"], out["dtype"] = "GEMM TFLOP/s (2 m n k per call)", "bf16"
+            out["config"] = {"workload": cases[1]["workload"]}
             out["value"], out["unit"], out["ms_per_step"] = cases[1]["value"], "TFLOP/s", cases[1]["ms"]
+
+    if args.only in ("all", "io"):
+        cases = run_io(T)
+        ceil = {"h2d": cases[4]["value"], "d2h": cases[5]["value"]}
+        for c in cases[:4]:
+            c["frac_of_pinned_dma"] = c["value"] / ceil["h2d" if c["workload"].startswith("h2d") else "d2h"]
+        out["io"] = {"bytes": IO_BYTES, "cases": cases}
+        if args.only == "io":
+            out["metric"], out["dtype"] = "host -> device staged copy GB/s", "f32"
+            out["config"] = {"workload": cases[0]["workload"], "bytes": IO_BYTES}
+            out["data"] = "synthetic (host N(0,1) numpy array)"
+            out["value"], out["unit"], out["ms_per_step"] = cases[0]["value"], "GB/s", cases[0]["ms"]
 
     if args.only == "all":
         # context for roofline.frac: what a tuned library GEMM sustains on real data,

@@ -71,10 +71,29 @@ int tt_mem_stats(size_t* in_use, size_t* cached);
 
 /* Copies ordered on the library stream.  d2h and h2d return after the copy
  * completed (the reference's copies are synchronous: src/Tinytensor.cu:40,61,
- * 213,238,251).  d2d is stream-ordered (src/Tinytensor.cu:78,125,189,377). */
+ * 213,238,251).  d2d is stream-ordered (src/Tinytensor.cu:78,125,189,377).
+ * h2d / d2h of 4 MiB or more from pageable host memory run through pinned
+ * staging buffers (16 MiB x 3, allocated on first use and kept), copied by
+ * up to TT_HOST_THREADS host threads (default min(16, CPUs in the process's
+ * affinity mask)) while the DMA engine moves the previous chunk; pinned host
+ * memory is copied directly. */
 int tt_memcpy_h2d(void* dst, const void* src, size_t bytes);
 int tt_memcpy_d2h(void* dst, const void* src, size_t bytes);
 int tt_memcpy_d2d(void* dst, const void* src, size_t bytes);
+/* Converting copies for bf16 storage (no counterpart in the reference, which
+ * has no bf16 tensors; they replace its upload/download of host values,
+ * src/Tinytensor.cu:40,213): n float32 host values rounded to nearest even
+ * into n bf16 on the device (NaN stays NaN), and n device bf16 widened into
+ * float32 host values.  The conversion runs in the staging pass above;
+ * synchronous like tt_memcpy_h2d / tt_memcpy_d2h. */
+int tt_upload_bf16_from_f32(void* dst, const float* src, size_t n);
+int tt_download_bf16_to_f32(float* dst, const void* src, size_t n);
+/* Pinned (page-locked) host memory, as cudaMallocHost / cudaFreeHost (the
+ * reference allocates none; it is here so that callers can hand
+ * tt_memcpy_h2d / tt_memcpy_d2h memory the DMA engine reads directly).
+ * tt_host_free(NULL) is a no-op. */
+int tt_host_malloc(void** ptr, size_t bytes);
+int tt_host_free(void* ptr);
 /* Byte fill (src/Tinytensor.cu:300 cudaMemset). */
 int tt_memset(void* ptr, int value, size_t bytes);
 /* Wait for all work on the library stream. */

@@ -29,7 +29,10 @@ CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 INCLUDE = os.path.join(ROOT, "include")
 
-HIP_SOURCES = ["tt_runtime.hip", "attn_fwd.hip", "attn_bwd.hip", "attn_decode.hip", "softmax.hip", "gemm.hip"]
+HIP_SOURCES = ["tt_runtime.hip", "attn_fwd.hip", "attn_bwd.hip", "attn_decode.hip", "softmax.hip", "gemm.hip",
+               "staging.hip"]
+# Host-only C++ linked into libtt_hip.so (the staged transfers' copy loops).
+LIB_HOST_SOURCES = ["host_copy.cpp"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 # Packed-FP32 instructions are kept out of every kernel; the host pass warns
 # that it does not know the feature, which is harmless.
@@ -91,11 +94,17 @@ def build(verbose: bool = False) -> dict:
         _run([CXX, *cxx_flags, "-c", os.path.join(CSRC, src), "-o", obj], verbose)
         return obj
 
+    def lib_obj(src):
+        obj = os.path.join(OBJ, src.replace(".cpp", ".o"))
+        _run([CXX, "-O3", "-fPIC", "-std=c++17", "-Wall", "-c", os.path.join(CSRC, src), "-o", obj], verbose)
+        return obj
+
     host_sources = ["tinytensor.cpp", "layers.cpp", "bind_tensor.cpp", "bind_layer.cpp"]
     with ThreadPoolExecutor(max_workers=_jobs()) as ex:
         hip_futs = [ex.submit(hip_obj, s) for s in HIP_SOURCES]
+        lib_futs = [ex.submit(lib_obj, s) for s in LIB_HOST_SOURCES]
         cxx_futs = {s: ex.submit(cxx_obj, s) for s in host_sources}
-        hip_objs = [f.result() for f in hip_futs]
+        hip_objs = [f.result() for f in hip_futs] + [f.result() for f in lib_futs]
         cxx_objs = {s: f.result() for s, f in cxx_futs.items()}
 
     tmp = paths["libtt_hip"] + ".tmp"

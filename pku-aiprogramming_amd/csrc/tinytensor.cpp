@@ -41,6 +41,23 @@ static void check_device(const std::string& dev) {
   if (dev != "cpu" && dev != "gpu") throw std::invalid_argument("Invalid device");
 }
 
+// n host values -> device storage, and back; synchronous.  bf16 converts in
+// the library's staging pass; every other dtype stores its host type as is.
+template <typename T>
+static void upload(T* dev, const typename Dtype<T>::host* src, size_t n) {
+  if constexpr (std::is_same<T, bf16>::value)
+    tt_check(tt_upload_bf16_from_f32(dev, src, n), "TinyTensor upload");
+  else
+    tt_check(tt_memcpy_h2d(dev, src, n * sizeof(T)), "TinyTensor upload");
+}
+template <typename T>
+static void download(typename Dtype<T>::host* dst, const T* dev, size_t n) {
+  if constexpr (std::is_same<T, bf16>::value)
+    tt_check(tt_download_bf16_to_f32(dst, dev, n), "TinyTensor download");
+  else
+    tt_check(tt_memcpy_d2h(dst, dev, n * sizeof(T)), "TinyTensor download");
+}
+
 template <typename T>
 void TinyTensor<T>::allocate() {
   size = shape_size(shape);
@@ -78,12 +95,15 @@ TinyTensor<T>::TinyTensor(const std::vector<int>& shape_, const std::string& dev
   allocate();
   // Like the reference, copy min(size, data.size()) leading values; the rest
   // of the storage is zero here rather than uninitialised.
-  std::vector<T> staged(size);
-  for (size_t i = 0; i < size; ++i) staged[i] = Dtype<T>::from_host(i < data.size() ? data[i] : Host(0));
-  if (device == "cpu")
-    std::copy(staged.begin(), staged.end(), p_data);
-  else
-    tt_check(tt_memcpy_h2d(p_data, staged.data(), size * sizeof(T)), "TinyTensor upload");
+  if (device == "cpu") {
+    for (size_t i = 0; i < size; ++i) p_data[i] = Dtype<T>::from_host(i < data.size() ? data[i] : Host(0));
+  } else if (data.size() >= size) {
+    upload(p_data, data.data(), size);
+  } else {
+    std::vector<Host> padded(size, Host(0));
+    std::copy(data.begin(), data.end(), padded.begin());
+    upload(p_data, padded.data(), size);
+  }
 }
 
 template <typename T>
@@ -96,18 +116,10 @@ TinyTensor<T>::TinyTensor(const py::array_t<Host>& data, const std::string& devi
   for (auto dim : buf.shape) shape.push_back((int)dim);
   allocate();
   const Host* src = static_cast<const Host*>(buf.ptr);
-  if constexpr (std::is_same<T, Host>::value) {
-    if (device == "cpu")
-      std::copy(src, src + size, p_data);
-    else
-      tt_check(tt_memcpy_h2d(p_data, src, size * sizeof(T)), "TinyTensor upload");
+  if (device == "cpu") {
+    for (size_t i = 0; i < size; ++i) p_data[i] = Dtype<T>::from_host(src[i]);
   } else {
-    std::vector<T> staged(size);
-    for (size_t i = 0; i < size; ++i) staged[i] = Dtype<T>::from_host(src[i]);
-    if (device == "cpu")
-      std::copy(staged.begin(), staged.end(), p_data);
-    else
-      tt_check(tt_memcpy_h2d(p_data, staged.data(), size * sizeof(T)), "TinyTensor upload");
+    upload(p_data, src, size);
   }
 }
 
@@ -221,18 +233,12 @@ std::string TinyTensor<T>::get_device() const {
 
 template <typename T>
 std::vector<typename TinyTensor<T>::Host> TinyTensor<T>::get_data() const {
-  std::vector<T> raw(size);
+  std::vector<Host> out(size);
   if (device == "cpu")
-    std::copy(p_data, p_data + size, raw.begin());
+    for (size_t i = 0; i < size; ++i) out[i] = Dtype<T>::to_host(p_data[i]);
   else
-    tt_check(tt_memcpy_d2h(raw.data(), p_data, size * sizeof(T)), "TinyTensor download");
-  if constexpr (std::is_same<T, Host>::value) {
-    return raw;
-  } else {
-    std::vector<Host> out(size);
-    for (size_t i = 0; i < size; ++i) out[i] = Dtype<T>::to_host(raw[i]);
-    return out;
-  }
+    download(out.data(), p_data, size);
+  return out;
 }
 
 template <typename T>
@@ -240,19 +246,10 @@ py::array_t<typename TinyTensor<T>::Host> TinyTensor<T>::numpy() const {
   std::vector<py::ssize_t> dims(shape.begin(), shape.end());
   py::array_t<Host> out(dims);
   Host* dst = out.mutable_data();
-  if constexpr (std::is_same<T, Host>::value) {
-    if (device == "cpu")
-      std::copy(p_data, p_data + size, dst);
-    else
-      tt_check(tt_memcpy_d2h(dst, p_data, size * sizeof(T)), "TinyTensor download");
-  } else {
-    std::vector<T> raw(size);
-    if (device == "cpu")
-      std::copy(p_data, p_data + size, raw.begin());
-    else
-      tt_check(tt_memcpy_d2h(raw.data(), p_data, size * sizeof(T)), "TinyTensor download");
-    for (size_t i = 0; i < size; ++i) dst[i] = Dtype<T>::to_host(raw[i]);
-  }
+  if (device == "cpu")
+    for (size_t i = 0; i < size; ++i) dst[i] = Dtype<T>::to_host(p_data[i]);
+  else
+    download(dst, p_data, size);
   return out;
 }
 

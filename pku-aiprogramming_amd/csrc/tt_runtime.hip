@@ -336,25 +336,7 @@ int tt_mem_stats(size_t* in_use, size_t* cached) {
   return TT_OK;
 }
 
-int tt_memcpy_h2d(void* dst, const void* src, size_t bytes) {
-  if (bytes == 0) return TT_OK;
-  if (!dst || !src) return fail(TT_ERR_ARG, "tt_memcpy_h2d: null pointer");
-  int rc = ensure_init();
-  if (rc) return rc;
-  TT_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, g_stream));
-  TT_HIP(hipStreamSynchronize(g_stream));
-  return ok();
-}
-
-int tt_memcpy_d2h(void* dst, const void* src, size_t bytes) {
-  if (bytes == 0) return TT_OK;
-  if (!dst || !src) return fail(TT_ERR_ARG, "tt_memcpy_d2h: null pointer");
-  int rc = ensure_init();
-  if (rc) return rc;
-  TT_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, g_stream));
-  TT_HIP(hipStreamSynchronize(g_stream));
-  return ok();
-}
+// tt_memcpy_h2d / tt_memcpy_d2h: staging.hip
 
 int tt_memcpy_d2d(void* dst, const void* src, size_t bytes) {
   if (bytes == 0) return TT_OK;

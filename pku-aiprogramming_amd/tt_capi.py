@@ -40,6 +40,10 @@ _SIGS = {
     "tt_memcpy_h2d": (C.c_int, [_p, _p, C.c_size_t]),
     "tt_memcpy_d2h": (C.c_int, [_p, _p, C.c_size_t]),
     "tt_memcpy_d2d": (C.c_int, [_p, _p, C.c_size_t]),
+    "tt_upload_bf16_from_f32": (C.c_int, [_p, _p, C.c_size_t]),
+    "tt_download_bf16_to_f32": (C.c_int, [_p, _p, C.c_size_t]),
+    "tt_host_malloc": (C.c_int, [C.POINTER(_p), C.c_size_t]),
+    "tt_host_free": (C.c_int, [_p]),
     "tt_memset": (C.c_int, [_p, C.c_int, C.c_size_t]),
     "tt_sync": (C.c_int, []),
     "tt_event_create": (C.c_int, [C.POINTER(_p)]),
@@ -153,8 +157,15 @@ class DeviceBuffer:
         return b
 
     def upload(self, a: np.ndarray):
+        """Copy a host array in.  A bf16 buffer takes float values (rounded
+        to nearest even by tt_upload_bf16_from_f32) or uint16 bit patterns."""
+        if self.dtype == "bf16" and a.dtype != np.uint16:
+            host = np.ascontiguousarray(a, dtype=np.float32)
+            assert 2 * host.size == self.nbytes, (host.shape, self.shape)
+            self.L.call("tt_upload_bf16_from_f32", self.ptr, host.ctypes.data, host.size)
+            return
         if self.dtype == "bf16":
-            host = bf16_bits(a) if a.dtype != np.uint16 else np.ascontiguousarray(a)
+            host = np.ascontiguousarray(a)
         elif self.dtype == "f32":
             host = np.ascontiguousarray(a, dtype=np.float32)
         elif self.dtype == "i32":
@@ -165,13 +176,20 @@ class DeviceBuffer:
         self.L.call("tt_memcpy_h2d", self.ptr, host.ctypes.data, self.nbytes)
 
     def download(self) -> np.ndarray:
-        """Copy back; bf16 is returned as float32 values."""
+        """Copy back; bf16 is returned as float32 values (tt_download_bf16_to_f32)."""
         if self.dtype == "bf16":
-            raw = np.empty(self.shape, np.uint16)
-        else:
-            raw = np.empty(self.shape, {"f32": np.float32, "i32": np.int32, "f64": np.float64}[self.dtype])
+            out = np.empty(self.shape, np.float32)
+            self.L.call("tt_download_bf16_to_f32", out.ctypes.data, self.ptr, out.size)
+            return out
+        raw = np.empty(self.shape, {"f32": np.float32, "i32": np.int32, "f64": np.float64}[self.dtype])
         self.L.call("tt_memcpy_d2h", raw.ctypes.data, self.ptr, self.nbytes)
-        return bf16_to_f32(raw) if self.dtype == "bf16" else raw
+        return raw
+
+    def download_bytes(self) -> np.ndarray:
+        """The stored bytes as is (bf16 as uint16 bit patterns)."""
+        raw = np.empty(self.shape, {"f32": np.float32, "i32": np.int32, "f64": np.float64, "bf16": np.uint16}[self.dtype])
+        self.L.call("tt_memcpy_d2h", raw.ctypes.data, self.ptr, self.nbytes)
+        return raw
 
     def fill_normal(self, seed: int, scale: float = 1.0):
         code = TT_BF16 if self.dtype == "bf16" else TT_F32
