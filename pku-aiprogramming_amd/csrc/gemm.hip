@@ -39,6 +39,9 @@ constexpr int GM = 128;  // C tile rows per workgroup
 #ifndef TT_GEMM_WIDE
 #define TT_GEMM_WIDE 1
 #endif
+#ifndef TT_GEMM_SWZ
+#define TT_GEMM_SWZ 1
+#endif
 
 template <typename T>
 struct GemmT;
@@ -48,6 +51,7 @@ struct GemmT<float> {
   static constexpr int BK = 16, EPC = 4;  // k per step; elements per 16-byte chunk
   static constexpr int PAD_K = 4;         // [rows][BK + PAD_K]: 80-byte rows keep 16-byte stores aligned
   static constexpr int PAD_R = 4;         // [BK][rows + PAD_R]
+  static constexpr bool SWZ = false;      // k-contiguous tiles padded, not swizzled
   static __device__ __forceinline__ float to_f(float x) { return x; }
   static __device__ __forceinline__ float from_f(float x) { return x; }
 };
@@ -57,8 +61,21 @@ struct GemmT<u16> {
   // of 128 x 128 ones; BK = 32 keeps two workgroups' rings in LDS
   static constexpr int GN = TT_GEMM_WIDE ? 256 : 128;
   static constexpr int BK = TT_GEMM_WIDE ? 32 : 64, EPC = 8;
-  static constexpr int PAD_K = 8;   // row stride 144 B: 16 lanes of 16-byte row reads hit disjoint banks
-  static constexpr int PAD_R = 16;  // row stride 288 B: the 4 rows of a transpose read hit disjoint banks
+#if TT_GEMM_SWZ
+  // LDS has 64 banks of 4 bytes.  k-contiguous tiles: unpadded rows whose
+  // 16-byte chunks are XOR-swizzled by row, so that both the 16 rows of a
+  // 16-lane ds_read_b128 and the 4 rows x 4 chunks of a 16-lane store hit 16
+  // distinct 4-bank groups.  [BK][rows] tiles: row stride = 16 banks mod 64,
+  // so the 4 k-rows x 2 column halves read by 32 lanes of a transpose read
+  // cover the 64 banks once.
+  static constexpr int PAD_K = 0;
+  static constexpr int PAD_R = 32;
+  static constexpr bool SWZ = true;
+#else
+  static constexpr int PAD_K = 8;
+  static constexpr int PAD_R = 16;
+  static constexpr bool SWZ = false;
+#endif
   static __device__ __forceinline__ float to_f(u16 x) { return bf16_to_f32(x); }
   static __device__ __forceinline__ u16 from_f(float x) { return f32_to_bf16(x); }
 };
@@ -75,6 +92,15 @@ struct OpTile {
   // LDS: KC ? [R][BK + PAD_K] : [BK][R + PAD_R]
   static constexpr int LD = KC ? BK + G::PAD_K : R + G::PAD_R;
   static constexpr int ELEMS = KC ? R * LD : BK * LD;
+  static constexpr bool SWZ = KC && G::SWZ;
+  static constexpr int NCH = BK / EPC;                    // 16-byte chunks per k-contiguous row
+  static constexpr int RPB = NCH >= 16 ? 1 : 16 / NCH;    // rows per 64 banks
+
+  // Element offset of chunk c (EPC elements) of tile row r.
+  __device__ static __forceinline__ int chunk_off(int r, int c) {
+    if constexpr (SWZ) return r * LD + ((c ^ ((r / RPB) % NCH)) * EPC);
+    return r * LD + c * EPC;
+  }
 
   typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
   u32x4 reg[CH];
@@ -117,7 +143,8 @@ struct OpTile {
     for (int c = 0; c < CH; ++c) {
       int srow, scol;
       chunk_pos(c, srow, scol);
-      *reinterpret_cast<u32x4*>(&s[srow * LD + scol]) = reg[c];
+      const int off = KC ? chunk_off(srow, scol / EPC) : srow * LD + scol;
+      *reinterpret_cast<u32x4*>(&s[off]) = reg[c];
     }
   }
 };
@@ -132,7 +159,7 @@ __device__ __forceinline__ auto operand(const T* s, int rbase, int ks) {
   if constexpr (sizeof(T) == 2) {
     const int k0 = 16 * ks;
     if constexpr (KC) {
-      return *reinterpret_cast<const bf16x8*>(&s[(rbase + (l & 31)) * Tile::LD + k0 + 8 * (l >> 5)]);
+      return *reinterpret_cast<const bf16x8*>(&s[Tile::chunk_off(rbase + (l & 31), k0 / 8 + (l >> 5))]);
     } else {
       // transpose reads: 16-lane group G = l / 16 takes rows (k) k0 + 8(G/2) + 0..3
       // (then + 4..7) of columns rbase + 16(G%2) + 0..15; lane s of the group
