@@ -48,10 +48,10 @@ C4 = dict(B=64, H=32, Lkv=8192, d=128)
 # write x1.000); the commands and raw counters are in
 # profiles/hbm_traffic_c5_c4.md.  Re-measured whenever a kernel changes.
 MEASURED_TRAFFIC_MIB = {
-    "attn_fwd": 524.9,
+    "attn_fwd": 580.7,
     "attn_bwd_delta": 264.0,
-    "attn_bwd_dkdv": 3130.6,   # includes the 2.06 GiB of dS it stores for the dQ GEMM
-    "attn_bwd_dq": 2571.3,     # the dQ GEMM: reads that dS back
+    "attn_bwd_dkdv": 3072.4,   # includes the 2.06 GiB of dS it stores for the dQ GEMM
+    "attn_bwd_dq": 2369.0,     # the dQ GEMM: reads that dS back
     "attn_decode_split": 8217.7,
     "softmax_reg": 2048.1,     # k_softmax_reg<16>, 262144 x 1024 fp32 (profiles/softmax_rows_kernel_stats.md)
 }

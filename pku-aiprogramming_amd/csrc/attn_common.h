@@ -192,6 +192,12 @@ __device__ __forceinline__ void glds16(const void* sbase, uint32_t voff, uint32_
   asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds)
                : "memory", "m0");
 }
+// Same, marked non-temporal: data read once (streamed), kept out of the way
+// of data that is reused from L2.
+__device__ __forceinline__ void glds16_nt(const void* sbase, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1 nt" ::"v"(voff), "s"(sbase), "s"(lds)
+               : "memory", "m0");
+}
 __device__ __forceinline__ void glds4(const void* sbase, uint32_t voff, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(sbase), "s"(lds)
                : "memory", "m0");
