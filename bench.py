@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X TinyTensor attention path (one GPU).
 
-Headline workload (BASELINE.json ``configs[4]``, the MFMA-utilisation
+Headline workload (configuration c5, the MFMA-utilisation
 config): causal attention forward + backward, bf16 inputs with fp32
 accumulation, B=4, H=32, L=4096, d=128.  One step = one forward
 (``tt_attn_fwd_bf16``) plus one backward (``tt_attn_bwd_bf16``) over inputs
@@ -22,7 +22,8 @@ gradient rules) restated in float32 numpy by ``oracle/attn_oracle.py`` --
 timed on a bounded sample of the same workload's heads on the host cores.
 
 Prints ONE JSON line.  ``--gpus N`` with N > 1 exits: this build runs on one
-GPU (heads shard across GPUs without exchange; see the design notes).
+GPU (the (b, h) heads shard across GPUs with no exchange, so N GPUs would run
+N independent shares of the same kernels).
 """
 from __future__ import annotations
 
