@@ -336,12 +336,7 @@ def cpu_baseline(sample_heads):
 
     from oracle import attn_oracle as orc
 
-    try:
-        from threadpoolctl import threadpool_info
-
-        cores = max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
-    except Exception:
-        cores = os.cpu_count() or 1
+    cores = _blas_threads()
     L, d = C5["L"], C5["d"]
     scale = float(np.float32(1.0 / math.sqrt(d)))
     rng = np.random.default_rng(5)
@@ -367,6 +362,52 @@ def cpu_baseline(sample_heads):
                   f"fwd+bwd, bf16-valued inputs in fp32, reference op order (full L x L materialised); "
                   f"{t:.2f} s",
     }
+
+
+def _blas_threads():
+    try:
+        from threadpoolctl import threadpool_info
+
+        return max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
+    except Exception:
+        return os.cpu_count() or 1
+
+
+def gemm_cpu_baseline(n=2048, reps=3):
+    """The reference's CPU matmul (MatMul.compute = np.matmul in float32,
+    optimizer/operators.py:416-419) on the host's BLAS threads."""
+    import numpy as np
+
+    rng = np.random.default_rng(0)
+    a = rng.standard_normal((n, n), dtype=np.float32)
+    b = rng.standard_normal((n, n), dtype=np.float32)
+    np.matmul(a, b)
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        np.matmul(a, b)
+        ts.append(time.perf_counter() - t0)
+    t = sorted(ts)[len(ts) // 2]
+    return {"value": 2.0 * n ** 3 / t / 1e12, "unit": "TFLOP/s", "cores": int(_blas_threads()), "kind": "port",
+            "sample": f"fp32 {n}^3 np.matmul (median of {reps}: {t * 1e3:.1f} ms)"}
+
+
+def io_cpu_baseline(T, nbytes=16 << 20):
+    """The reference's download path: get_data() (a synchronous copy into a
+    std::vector, then a Python list) and np.array of that list, as its
+    operators do (optimizer/operators.py:482,511)."""
+    import numpy as np
+
+    import myTensor as mt
+
+    x = np.random.default_rng(0).standard_normal(nbytes // 4, dtype=np.float32).reshape(1, -1)
+    t = mt.Tensor_float(x, "gpu")
+    np.array(t.get_data())
+    t0 = time.perf_counter()
+    np.array(t.get_data())
+    dt = time.perf_counter() - t0
+    return {"value": nbytes / dt / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"{nbytes >> 20} MiB fp32 tensor, np.array(t.get_data()) ({dt * 1e3:.0f} ms)"}
 
 
 def main(argv=None):
@@ -486,6 +527,8 @@ def main(argv=None):
             cases.append({"workload": f"{c['dtype']} {c['m']}x{c['n']}x{c['k']} ta={int(c['ta'])} tb={int(c['tb'])}",
                           "ms": ms, "value": tf, "unit": "TFLOP/s", "frac_of_peak": tf / peak, "peak": peak})
         out["gemm"] = {"cases": cases}
+        if not args.no_cpu_baseline:
+            out["gemm"]["cpu_baseline"] = gemm_cpu_baseline()
         if args.only == "gemm":
             out["metric"], out["dtype"] = "GEMM TFLOP/s (2 m n k per call)", "bf16"
             out["config"] = {"workload": cases[1]["workload"]}
@@ -497,6 +540,8 @@ def main(argv=None):
         for c in cases[:4]:
             c["frac_of_pinned_dma"] = c["value"] / ceil["h2d" if c["workload"].startswith("h2d") else "d2h"]
         out["io"] = {"bytes": IO_BYTES, "cases": cases}
+        if not args.no_cpu_baseline:
+            out["io"]["cpu_baseline"] = io_cpu_baseline(T)
         if args.only == "io":
             out["metric"], out["dtype"] = "host -> device staged copy GB/s", "f32"
             out["config"] = {"workload": cases[0]["workload"], "bytes": IO_BYTES}
