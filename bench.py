@@ -54,7 +54,8 @@ MEASURED_TRAFFIC_MIB = {
     "attn_bwd_dkdv": 3072.4,   # includes the 2.06 GiB of dS it stores for the dQ GEMM
     "attn_bwd_dq": 2369.0,     # the dQ GEMM: reads that dS back
     "attn_decode_split": 8217.7,
-    "softmax_reg": 2048.1,     # k_softmax_reg<16>, 262144 x 1024 fp32 (profiles/softmax_rows_kernel_stats.md)
+    "softmax_reg": 2048.1,
+    "gemm_bf16_nn": 1536.5 + 143.0,  # k_gemm<u16> 8192^3 NN (profiles/gemm_kernel_stats.md)     # k_softmax_reg<16>, 262144 x 1024 fp32 (profiles/softmax_rows_kernel_stats.md)
 }
 
 
@@ -526,13 +527,19 @@ def main(argv=None):
             peak = PEAK_BF16_TFLOPS if c["dtype"] == "bf16" else PEAK_FP32_MFMA_TFLOPS
             cases.append({"workload": f"{c['dtype']} {c['m']}x{c['n']}x{c['k']} ta={int(c['ta'])} tb={int(c['tb'])}",
                           "ms": ms, "value": tf, "unit": "TFLOP/s", "frac_of_peak": tf / peak, "peak": peak})
-        out["gemm"] = {"cases": cases}
+        bf = cases[1]
+        out["gemm"] = {"cases": cases,
+                       "roofline": {"bound": "mfma", "kernel": "k_gemm<u16> " + bf["workload"],
+                                    "achieved": bf["value"], "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                                    "frac": bf["value"] / PEAK_BF16_TFLOPS,
+                                    "traffic": MEASURED_TRAFFIC_MIB["gemm_bf16_nn"] * 2 ** 20}}
         if not args.no_cpu_baseline:
             out["gemm"]["cpu_baseline"] = gemm_cpu_baseline()
         if args.only == "gemm":
             out["metric"], out["dtype"] = "GEMM TFLOP/s (2 m n k per call)", "bf16"
             out["config"] = {"workload": cases[1]["workload"]}
             out["value"], out["unit"], out["ms_per_step"] = cases[1]["value"], "TFLOP/s", cases[1]["ms"]
+            out["roofline"] = out["gemm"]["roofline"]
 
     if args.only in ("all", "io"):
         cases = run_io(T)
