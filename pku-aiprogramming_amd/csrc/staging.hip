@@ -268,12 +268,19 @@ int staged_d2h(char* dst, const char* src, size_t n, Cvt c, hipStream_t s) {
   return ok();
 }
 
-// True when p is host memory that HIP already holds pinned.
-bool host_pinned(const void* p) {
+// What HIP knows of the host-side pointer of a copy: pinned host memory
+// (copied directly), device memory (an argument error: the host threads of
+// the staged path cannot touch it), or ordinary pageable memory.
+enum class HostMem { kPageable, kPinned, kDevice };
+HostMem host_mem(const void* p) {
   hipPointerAttribute_t a;
-  const bool pinned = hipPointerGetAttributes(&a, p) == hipSuccess && a.type == hipMemoryTypeHost;
+  HostMem m = HostMem::kPageable;
+  if (hipPointerGetAttributes(&a, p) == hipSuccess) {
+    if (a.type == hipMemoryTypeHost) m = HostMem::kPinned;
+    else if (a.type == hipMemoryTypeDevice) m = HostMem::kDevice;
+  }
   (void)hipGetLastError();
-  return pinned;
+  return m;
 }
 
 // A failed staged copy may leave a DMA in flight on a pinned buffer: wait for
@@ -294,7 +301,9 @@ int tt_memcpy_h2d(void* dst, const void* src, size_t bytes) {
   int rc = ensure_init();
   if (rc) return rc;
   hipStream_t s = stream_or_default(nullptr);
-  if (bytes < kDirectMax || host_pinned(src)) {
+  const HostMem hm = host_mem(src);
+  if (hm == HostMem::kDevice) return fail(TT_ERR_ARG, "tt_memcpy_h2d: source is device memory (use tt_memcpy_d2d)");
+  if (bytes < kDirectMax || hm == HostMem::kPinned) {
     TT_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, s));
     TT_HIP(hipStreamSynchronize(s));
     return ok();
@@ -309,7 +318,10 @@ int tt_memcpy_d2h(void* dst, const void* src, size_t bytes) {
   int rc = ensure_init();
   if (rc) return rc;
   hipStream_t s = stream_or_default(nullptr);
-  if (bytes < kDirectMax || host_pinned(dst)) {
+  const HostMem hm = host_mem(dst);
+  if (hm == HostMem::kDevice)
+    return fail(TT_ERR_ARG, "tt_memcpy_d2h: destination is device memory (use tt_memcpy_d2d)");
+  if (bytes < kDirectMax || hm == HostMem::kPinned) {
     TT_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, s));
     TT_HIP(hipStreamSynchronize(s));
     return ok();
@@ -323,6 +335,7 @@ int tt_upload_bf16_from_f32(void* dst, const float* src, size_t n) {
   if (!dst || !src) return fail(TT_ERR_ARG, "tt_upload_bf16_from_f32: null pointer");
   int rc = ensure_init();
   if (rc) return rc;
+  if (host_mem(src) == HostMem::kDevice) return fail(TT_ERR_ARG, "tt_upload_bf16_from_f32: source is device memory");
   hipStream_t s = stream_or_default(nullptr);
   std::lock_guard<std::mutex> lk(g_stage_mu);
   return settle(staged_h2d((char*)dst, (const char*)src, n, Cvt::kF32ToBf16, s), s);
@@ -333,6 +346,8 @@ int tt_download_bf16_to_f32(float* dst, const void* src, size_t n) {
   if (!dst || !src) return fail(TT_ERR_ARG, "tt_download_bf16_to_f32: null pointer");
   int rc = ensure_init();
   if (rc) return rc;
+  if (host_mem(dst) == HostMem::kDevice)
+    return fail(TT_ERR_ARG, "tt_download_bf16_to_f32: destination is device memory");
   hipStream_t s = stream_or_default(nullptr);
   std::lock_guard<std::mutex> lk(g_stage_mu);
   return settle(staged_d2h((char*)dst, (const char*)src, n, Cvt::kBf16ToF32, s), s);

@@ -181,3 +181,22 @@ def test_tensor_large_round_trips(dt):
     # the list constructor pads with zeros past the data
     t = T([2, 3], "gpu", [1.5, 2.0, 3.00390625])
     np.testing.assert_array_equal(np.asarray(t.get_data(), np.float32), [1.5, 2.0, 3.0, 0, 0, 0])
+
+
+def test_device_pointer_as_host_side_is_an_error(capi):
+    """A device pointer passed where host memory belongs is refused before
+    any copy (the staged path's host threads could not touch it)."""
+    a = capi.DeviceBuffer((8 * MIB,), "i32")
+    b = capi.DeviceBuffer((8 * MIB,), "i32")
+    L = capi.lib()
+    for fn, args in (("tt_memcpy_h2d", (a.ptr, b.ptr, 32 * MIB)), ("tt_memcpy_d2h", (a.ptr, b.ptr, 32 * MIB)),
+                     ("tt_memcpy_h2d", (a.ptr, b.ptr, 64)),
+                     ("tt_upload_bf16_from_f32", (a.ptr, b.ptr, 1000)),
+                     ("tt_download_bf16_to_f32", (a.ptr, b.ptr, 1000))):
+        with pytest.raises(capi.TTError) as ei:
+            L.call(fn, *args)
+        assert ei.value.code == capi.TT_ERR_ARG and "device memory" in str(ei.value)
+    # the library still works afterwards
+    x = _bytes(4096, 5)
+    L.call("tt_memcpy_h2d", a.ptr, x.ctypes.data, 4096)
+    np.testing.assert_array_equal(a.download_bytes().view(np.uint8)[:4096], x)
