@@ -199,6 +199,46 @@ def test_c4_bf16_decode(capi):
     assert abs(float(np.std(qh)) - 1.0) < 0.05  # the generator is N(0,1)
 
 
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_decode_large_grid_ragged_last_split(capi, dtype):
+    """A grid large enough for the 1024-key splits, with a partial last split
+    (Lkv = 9000): every head against the forward kernel run with Lq = 1, and
+    sampled heads against the oracle."""
+    B, H, Lkv, d = 8, 64, 9000, 64
+    scale = float(np.float32(1.0 / math.sqrt(d)))
+    _say(f"decode {dtype} B={B} H={H} Lkv={Lkv} d={d} (1024-key splits, ragged last)")
+    q = capi.DeviceBuffer((B, H, 1, d), dtype)
+    k = capi.DeviceBuffer((B, H, Lkv, d), dtype)
+    v = capi.DeviceBuffer((B, H, Lkv, d), dtype)
+    q.fill_normal(50)
+    k.fill_normal(51)
+    v.fill_normal(52)
+    o = capi.DeviceBuffer((B, H, 1, d), dtype)
+    lse = capi.DeviceBuffer((B, H), "f32")
+    capi.attn_decode(q, k, v, o, lse, scale)
+    o2 = capi.DeviceBuffer((B, H, 1, d), dtype)
+    lse2 = capi.DeviceBuffer((B, H, 1), "f32")
+    capi.attn_fwd(q, k, v, o2, lse2, scale, False)
+    capi.lib().sync()
+    od, ld = o.download(), lse.download()
+    _check("decode vs forward kernel O", od, o2.download(), TOL[dtype])
+    _check("decode vs forward kernel LSE", ld, lse2.download()[..., 0], 2.0 ** -9)
+    qh = q.download()
+    esz = 2 if dtype == "bf16" else 4
+    import ctypes as C
+    for (bb, hh) in [(0, 0), (5, 37), (7, 63)]:
+        bh = bb * H + hh
+        slab = Lkv * d
+        raw = np.empty(slab, np.uint16 if dtype == "bf16" else np.float32)
+        heads = []
+        for buf in (k, v):
+            capi.lib().call("tt_memcpy_d2h", raw.ctypes.data, C.c_void_p(buf.ptr + esz * bh * slab), esz * slab)
+            heads.append((capi.bf16_to_f32(raw) if dtype == "bf16" else raw.copy()).reshape(Lkv, d))
+        o_ref, l_ref = orc.attn_decode_f64(qh[bb, hh], heads[0], heads[1], scale)
+        _check(f"head ({bb},{hh}) o", od[bb, hh], o_ref, TOL[dtype])
+        _check(f"head ({bb},{hh}) lse", ld[bb, hh], l_ref[0], TOL[dtype])
+
+
 # ------------------------------------------------------------------ shapes and edges
 
 SHAPES = [
