@@ -53,7 +53,7 @@ MEASURED_TRAFFIC_MIB = {
     "attn_bwd_delta": 264.0,
     "attn_bwd_dkdv": 3072.4,   # includes the 2.06 GiB of dS it stores for the dQ GEMM
     "attn_bwd_dq": 2369.0,     # the dQ GEMM: reads that dS back
-    "attn_decode_split": 8217.7,
+    "attn_decode_split": 8209.1,
     "softmax_reg": 2048.1,
     "gemm_bf16_nn": 1536.5 + 143.0,  # k_gemm<u16> 8192^3 NN (profiles/gemm_kernel_stats.md)     # k_softmax_reg<16>, 262144 x 1024 fp32 (profiles/softmax_rows_kernel_stats.md)
 }
