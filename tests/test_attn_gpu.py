@@ -199,6 +199,29 @@ def test_c4_bf16_decode(capi):
     assert abs(float(np.std(qh)) - 1.0) < 0.05  # the generator is N(0,1)
 
 
+def test_long_sequence_few_heads_bf16(capi):
+    """L = 8192 with only two heads (B*H not a multiple of 8: no per-XCD head
+    grouping; 64 query tiles per head; a 128 MiB stored-dS workspace): one
+    head against the float64 oracle, both through the identities."""
+    B, H, L, d = 1, 2, 8192, 128
+    _say("long sequence: bf16 causal B=1 H=2 L=8192 d=128")
+    rng = np.random.default_rng(8192)
+    x = {n: orc.bf16_round(rng.standard_normal((B, H, L, d), dtype=np.float32)) for n in ("q", "k", "v", "do")}
+    scale = float(np.float32(1.0 / math.sqrt(d)))
+    b = _run_fwd(capi, x, "bf16", scale, True)
+    o, lse = b["o"].download(), b["lse"].download()
+    dq, dk, dv = _run_bwd(capi, b, x["do"], "bf16", scale, True)
+    _identities("long", x, o, lse, dq, dk, dv, scale, True, TOL["bf16"])
+    one = {n: a[:, 1:2] for n, a in x.items()}
+    o_ref, l_ref = orc.attn_fwd_f64(one["q"], one["k"], one["v"], scale, True)
+    _check("head 1 O", o[:, 1:2], o_ref, TOL["bf16"])
+    _check("head 1 LSE", lse[:, 1:2], l_ref, TOL["bf16"])
+    rq, rk, rv = orc.attn_bwd_f64(one["q"], one["k"], one["v"], one["do"], scale, True)
+    _check("head 1 dQ", dq[:, 1:2], rq, TOL["bf16"])
+    _check("head 1 dK", dk[:, 1:2], rk, TOL["bf16"])
+    _check("head 1 dV", dv[:, 1:2], rv, TOL["bf16"])
+
+
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 def test_decode_large_grid_ragged_last_split(capi, dtype):
     """A grid large enough for the 1024-key splits, with a partial last split
