@@ -55,7 +55,7 @@ MEASURED_TRAFFIC_MIB = {
     "attn_bwd_dq": 2369.0,     # the dQ GEMM: reads that dS back
     "attn_decode_split": 8209.1,
     "softmax_reg": 2048.1,
-    "gemm_bf16_nn": 1536.5 + 143.0,  # k_gemm<u16> 8192^3 NN (profiles/gemm_kernel_stats.md)     # k_softmax_reg<16>, 262144 x 1024 fp32 (profiles/softmax_rows_kernel_stats.md)
+    "gemm_bf16_nn": 2527.8 + 149.6,  # k_gemm_dma 8192^3 NN (profiles/gemm_kernel_stats.md)     # k_softmax_reg<16>, 262144 x 1024 fp32 (profiles/softmax_rows_kernel_stats.md)
 }
 
 
@@ -529,7 +529,7 @@ def main(argv=None):
                           "ms": ms, "value": tf, "unit": "TFLOP/s", "frac_of_peak": tf / peak, "peak": peak})
         bf = cases[1]
         out["gemm"] = {"cases": cases,
-                       "roofline": {"bound": "mfma", "kernel": "k_gemm<u16> " + bf["workload"],
+                       "roofline": {"bound": "mfma", "kernel": "k_gemm_dma " + bf["workload"],
                                     "achieved": bf["value"], "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                                     "frac": bf["value"] / PEAK_BF16_TFLOPS,
                                     "traffic": MEASURED_TRAFFIC_MIB["gemm_bf16_nn"] * 2 ** 20}}

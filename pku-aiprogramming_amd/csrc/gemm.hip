@@ -11,6 +11,9 @@
 // beta = 0 does not read C.  fp32 on v_mfma_f32_32x32x2f32 (fp32 products,
 // fp32 sums) and bf16 on v_mfma_f32_32x32x16_bf16 (fp32 sums, bf16 C).
 //
+// bf16 calls whose tiles are all full (m % 128, n % 256, k % 32 == 0, aligned)
+// run k_gemm_dma: direct global -> LDS tile loads into swizzled, unpadded
+// tiles.  Every other call runs k_gemm:
 // Workgroup = 4 waves, a 128 x 128 (fp32) or 128 x 256 (bf16) tile of C
 // (each wave 64 x 64 or 64 x 128: 2 x 2 or 2 x 4 MFMA blocks of 32 x 32);
 // k in steps of BK through a two-stage LDS ring,
@@ -256,6 +259,134 @@ __global__ __launch_bounds__(256, 2) void k_gemm(int M, int N, int K, float alph
     }
 }
 
+// The direct-to-LDS kernel below serves full bf16 tiles (1); 0 sends every
+// call to k_gemm.  A 2-deep ring (48 KB of LDS, 155-167 VGPRs: three
+// workgroups per CU) measured 1075-1093 TF at 8192^3 against 985-1018 for 3
+// stages and 845-892 for 4 (one or two workgroups per CU).
+#ifndef TT_GEMM_DMA
+#define TT_GEMM_DMA 1
+#endif
+#ifndef TT_GEMM_DMA_S
+#define TT_GEMM_DMA_S 2
+#endif
+
+// bf16 full-tile kernel (m % 128 == 0, n % 256 == 0, k % 32 == 0, 16-byte
+// aligned operands): tiles go straight from global memory into LDS
+// (global_load_lds_dwordx4, no register staging) through an S-deep ring, in
+// unpadded XOR-swizzled layouts that the 64 contiguous 16-byte slots of a
+// wave's load instruction can fill:
+//   k contiguous ([rows][32], 64-byte rows): chunk c of row r at c ^ ((r >> 2) & 3);
+//   rows contiguous ([32][rows], 256- or 512-byte k-rows): chunk c of k-row r at
+//   c ^ ((r & 3) << 2).
+// Both keep the MFMA operand reads (16-byte row reads, transpose reads) free
+// of bank conflicts.
+template <int R, bool KC>
+struct DmaTile {
+  static constexpr int BK = 32;
+  static constexpr int NCH = KC ? BK / 8 : R / 8;  // 16-byte chunks per stored row
+  static constexpr int ELEMS = R * BK;
+  static constexpr int LOADS = ELEMS / 8 / 256;    // load instructions per wave per tile
+  __device__ static __forceinline__ int pos(int row, int c) {
+    return KC ? (c ^ ((row >> 2) & 3)) : (c ^ ((row & 3) << 2));
+  }
+  // element offset of chunk c of stored row `row`
+  __device__ static __forceinline__ int off(int row, int c) { return row * NCH * 8 + pos(row, c) * 8; }
+  // Load the tile whose first stored element is `src` (leading dimension ld)
+  // into `dst`: slot p of the workgroup's instruction i holds stored row
+  // p / NCH, chunk position p % NCH.
+  __device__ static __forceinline__ void load(const u16* src, int64_t ld, u16* dst) {
+    const int w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6), l = threadIdx.x & 63;
+#pragma unroll
+    for (int i = 0; i < LOADS; ++i) {
+      const int p = (i * 4 + w) * 64 + l, row = p / NCH, ps = p % NCH;
+      const int c = KC ? (ps ^ ((row >> 2) & 3)) : (ps ^ ((row & 3) << 2));  // the swizzle is an involution
+      glds16(src, (uint32_t)(2 * ((int64_t)row * ld + 8 * c)), lds_addr(dst) + 1024u * (uint32_t)(i * 4 + w));
+    }
+  }
+};
+
+template <int R, bool KC>
+__device__ __forceinline__ bf16x8 dma_operand(const u16* s, int rbase, int ks) {
+  using Tile = DmaTile<R, KC>;
+  const int l = threadIdx.x & 63;
+  if constexpr (KC) {
+    return *reinterpret_cast<const bf16x8*>(&s[Tile::off(rbase + (l & 31), 2 * ks + (l >> 5))]);
+  } else {
+    const int G = l >> 4, sl = l & 15;
+    const int kr = 16 * ks + 8 * (G >> 1) + (sl >> 2);
+    const int col = rbase + 16 * (G & 1) + 4 * (sl & 3);
+    return lds_read_tr16x2(&s[Tile::off(kr, col >> 3) + (col & 4)], &s[Tile::off(kr + 4, col >> 3) + (col & 4)]);
+  }
+}
+
+template <bool TA, bool TB>
+__global__ __launch_bounds__(256, 3) void k_gemm_dma(int M, int N, int K, float alpha, const u16* __restrict__ A,
+                                                    int64_t lda, const u16* __restrict__ B, int64_t ldb,
+                                                    float beta, u16* C) {
+  using G = GemmT<u16>;
+  constexpr int GN = 256, NB = GN / 64, BK = 32, KS = BK / 16, S = TT_GEMM_DMA_S;
+  using TileA = DmaTile<GM, !TA>;
+  using TileB = DmaTile<GN, TB>;
+  constexpr int PER = TileA::LOADS + TileB::LOADS;
+  static_assert(PER * (S - 2) < 64, "vmcnt range");
+  __shared__ __align__(16) u16 sA[S][TileA::ELEMS];
+  __shared__ __align__(16) u16 sB[S][TileB::ELEMS];
+
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+  const int m0 = blockIdx.y * GM, n0 = blockIdx.x * GN;
+  const int wm = 64 * (w >> 1), wn = (GN / 2) * (w & 1);
+  f32x16 acc[2][NB];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < NB; ++j) acc[i][j] = f32x16{};
+
+  const int nk = K / BK;
+  // stored origin of k-step t: A as stored is [m][k] (TA = 0) or [k][m]
+  auto issue = [&](int t) {
+    const int k0 = BK * t, b = t % S;
+    TileA::load(TA ? A + (int64_t)k0 * lda + m0 : A + (int64_t)m0 * lda + k0, lda, sA[b]);
+    TileB::load(TB ? B + (int64_t)n0 * ldb + k0 : B + (int64_t)k0 * ldb + n0, ldb, sB[b]);
+  };
+#pragma unroll
+  for (int t = 0; t < S - 1; ++t)
+    if (t < nk) issue(t);
+  for (int t = 0; t < nk; ++t) {
+    wait_vmem_tiles<PER, (S - 2 < 3 ? S - 2 : 3)>(min(S - 2, nk - 1 - t));  // tile t has landed
+    __syncthreads();
+    if (t + S - 1 < nk) issue(t + S - 1);  // into the buffer every wave finished at step t - 1
+    const u16* a = sA[t % S];
+    const u16* bb = sB[t % S];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const bf16x8 a0 = dma_operand<GM, !TA>(a, wm, ks);
+      const bf16x8 a1 = dma_operand<GM, !TA>(a, wm + 32, ks);
+#pragma unroll
+      for (int j = 0; j < NB; ++j) {
+        const bf16x8 b = dma_operand<GN, TB>(bb, wn + 32 * j, ks);
+        acc[0][j] = mfma_bf16_32x32x16(a0, b, acc[0][j]);
+        acc[1][j] = mfma_bf16_32x32x16(a1, b, acc[1][j]);
+      }
+    }
+  }
+  wait_vmem_le<0>();  // nothing may be in flight into LDS when the workgroup exits
+
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      const int n = n0 + wn + 32 * j + (l & 31);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = m0 + wm + 32 * i + acc_row(r, l >> 5);
+        u16* p = C + (int64_t)m * N + n;
+        float v = alpha * acc[i][j][r];
+        if (beta != 0.f) v += beta * G::to_f(*p);
+        *p = G::from_f(v);
+      }
+    }
+}
+
 template <typename T>
 int gemm_launch(const char* fn, int transa, int transb, int64_t m, int64_t n, int64_t k, float alpha, const T* A,
                 const T* B, float beta, T* C, void* stream) {
@@ -276,6 +407,24 @@ int gemm_launch(const char* fn, int transa, int transb, int64_t m, int64_t n, in
   constexpr int EPC = GemmT<T>::EPC;
   const bool vec = lda % EPC == 0 && ldb % EPC == 0 && (uintptr_t)A % 16 == 0 && (uintptr_t)B % 16 == 0;
   const dim3 grid((unsigned)gx, (unsigned)gy), block(256);
+  if constexpr (sizeof(T) == 2) {
+    // full tiles, aligned, and every per-lane tile offset within 32 bits
+    if (TT_GEMM_DMA && vec && m % GM == 0 && n % 256 == 0 && k % 32 == 0 && lda < (int64_t(1) << 22) &&
+        ldb < (int64_t(1) << 22)) {
+      const dim3 g2((unsigned)(n / 256), (unsigned)(m / GM));
+#define TT_GEMM_D(TA, TB) \
+  hipLaunchKernelGGL((k_gemm_dma<TA, TB>), g2, dim3(256), 0, s, (int)m, (int)n, (int)k, alpha, A, lda, B, ldb, beta, C)
+      switch (transa * 2 + transb) {
+        case 0: TT_GEMM_D(false, false); break;
+        case 1: TT_GEMM_D(false, true); break;
+        case 2: TT_GEMM_D(true, false); break;
+        default: TT_GEMM_D(true, true); break;
+      }
+#undef TT_GEMM_D
+      TT_LAUNCHED(fn, s);
+      return ok();
+    }
+  }
 #define TT_GEMM(TA, TB, V)                                                                                   \
   hipLaunchKernelGGL((k_gemm<T, TA, TB, V>), grid, block, 0, s, (int)m, (int)n, (int)k, alpha, A, lda, B, ldb, \
                      beta, C)

@@ -57,6 +57,8 @@ def _run(capi, dt, ta, tb, m, n, k, alpha=1.0, beta=0.0, seed=0):
 SHAPES = [
     (1, 1, 1), (7, 5, 3), (128, 128, 64), (256, 128, 128), (129, 130, 65), (300, 257, 1000), (1000, 1, 37),
     (2, 3000, 17), (64, 64, 4096), (1024, 1024, 1024),
+    # full 128 x 256 tiles with k a multiple of 32 (the bf16 direct-to-LDS kernel)
+    (512, 768, 96), (128, 256, 32), (256, 512, 2048),
 ]
 
 
@@ -74,6 +76,7 @@ def test_gemm_alpha_beta_and_k0(capi, dt):
     _run(capi, dt, False, False, 200, 150, 96, alpha=0.5, beta=1.5)
     _run(capi, dt, True, True, 130, 70, 40, alpha=-2.0, beta=1.0)
     _run(capi, dt, False, True, 33, 65, 0, alpha=1.0, beta=3.0)   # k = 0: C = beta C
+    _run(capi, dt, True, False, 256, 512, 64, alpha=0.75, beta=-0.5)   # full tiles, C read
 
 
 def test_gemm_beta_zero_ignores_c(capi):
