@@ -11,9 +11,9 @@
 // beta = 0 does not read C.  fp32 on v_mfma_f32_32x32x2f32 (fp32 products,
 // fp32 sums) and bf16 on v_mfma_f32_32x32x16_bf16 (fp32 sums, bf16 C).
 //
-// bf16 calls whose tiles are all full (m % 128, n % 256, k % 32 == 0, aligned)
-// run k_gemm_dma: direct global -> LDS tile loads into swizzled, unpadded
-// tiles.  Every other call runs k_gemm:
+// bf16 calls with k % 32 == 0 and aligned operands run k_gemm_dma: direct
+// global -> LDS tile loads into swizzled, unpadded tiles.  Every other call
+// runs k_gemm:
 // Workgroup = 4 waves, a 128 x 128 (fp32) or 128 x 256 (bf16) tile of C
 // (each wave 64 x 64 or 64 x 128: 2 x 2 or 2 x 4 MFMA blocks of 32 x 32);
 // k in steps of BK through a two-stage LDS ring,
@@ -270,8 +270,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm(int M, int N, int K, float alph
 #define TT_GEMM_DMA_S 2
 #endif
 
-// bf16 full-tile kernel (m % 128 == 0, n % 256 == 0, k % 32 == 0, 16-byte
-// aligned operands): tiles go straight from global memory into LDS
+// bf16 kernel for k % 32 == 0 with 16-byte aligned operands (ragged m and n
+// allowed): tiles go straight from global memory into LDS
 // (global_load_lds_dwordx4, no register staging) through an S-deep ring, in
 // unpadded XOR-swizzled layouts that the 64 contiguous 16-byte slots of a
 // wave's load instruction can fill:
@@ -293,13 +293,19 @@ struct DmaTile {
   __device__ static __forceinline__ int off(int row, int c) { return row * NCH * 8 + pos(row, c) * 8; }
   // Load the tile whose first stored element is `src` (leading dimension ld)
   // into `dst`: slot p of the workgroup's instruction i holds stored row
-  // p / NCH, chunk position p % NCH.
-  __device__ static __forceinline__ void load(const u16* src, int64_t ld, u16* dst) {
+  // p / NCH, chunk position p % NCH.  `nr` tile rows (m or n) exist; slots of
+  // rows past them load the last one instead (a multiple of 8 when rows are
+  // the contiguous axis), so every address stays inside the matrix: those
+  // rows only feed C entries that are never stored.
+  __device__ static __forceinline__ void load(const u16* src, int64_t ld, int nr, u16* dst) {
     const int w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6), l = threadIdx.x & 63;
 #pragma unroll
     for (int i = 0; i < LOADS; ++i) {
-      const int p = (i * 4 + w) * 64 + l, row = p / NCH, ps = p % NCH;
-      const int c = KC ? (ps ^ ((row >> 2) & 3)) : (ps ^ ((row & 3) << 2));  // the swizzle is an involution
+      const int p = (i * 4 + w) * 64 + l, ps = p % NCH;
+      int row = p / NCH;
+      int c = KC ? (ps ^ ((row >> 2) & 3)) : (ps ^ ((row & 3) << 2));  // the swizzle is an involution
+      if (KC) row = min(row, nr - 1);
+      else c = min(c, nr / 8 - 1);
       glds16(src, (uint32_t)(2 * ((int64_t)row * ld + 8 * c)), lds_addr(dst) + 1024u * (uint32_t)(i * 4 + w));
     }
   }
@@ -345,8 +351,8 @@ __global__ __launch_bounds__(256, 3) void k_gemm_dma(int M, int N, int K, float 
   // stored origin of k-step t: A as stored is [m][k] (TA = 0) or [k][m]
   auto issue = [&](int t) {
     const int k0 = BK * t, b = t % S;
-    TileA::load(TA ? A + (int64_t)k0 * lda + m0 : A + (int64_t)m0 * lda + k0, lda, sA[b]);
-    TileB::load(TB ? B + (int64_t)n0 * ldb + k0 : B + (int64_t)k0 * ldb + n0, ldb, sB[b]);
+    TileA::load(TA ? A + (int64_t)k0 * lda + m0 : A + (int64_t)m0 * lda + k0, lda, M - m0, sA[b]);
+    TileB::load(TB ? B + (int64_t)n0 * ldb + k0 : B + (int64_t)k0 * ldb + n0, ldb, N - n0, sB[b]);
   };
 #pragma unroll
   for (int t = 0; t < S - 1; ++t)
@@ -376,9 +382,11 @@ __global__ __launch_bounds__(256, 3) void k_gemm_dma(int M, int N, int K, float 
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
       const int n = n0 + wn + 32 * j + (l & 31);
+      if (n >= N) continue;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int m = m0 + wm + 32 * i + acc_row(r, l >> 5);
+        if (m >= M) continue;
         u16* p = C + (int64_t)m * N + n;
         float v = alpha * acc[i][j][r];
         if (beta != 0.f) v += beta * G::to_f(*p);
@@ -408,10 +416,10 @@ int gemm_launch(const char* fn, int transa, int transb, int64_t m, int64_t n, in
   const bool vec = lda % EPC == 0 && ldb % EPC == 0 && (uintptr_t)A % 16 == 0 && (uintptr_t)B % 16 == 0;
   const dim3 grid((unsigned)gx, (unsigned)gy), block(256);
   if constexpr (sizeof(T) == 2) {
-    // full tiles, aligned, and every per-lane tile offset within 32 bits
-    if (TT_GEMM_DMA && vec && m % GM == 0 && n % 256 == 0 && k % 32 == 0 && lda < (int64_t(1) << 22) &&
-        ldb < (int64_t(1) << 22)) {
-      const dim3 g2((unsigned)(n / 256), (unsigned)(m / GM));
+    // k in whole steps, aligned rows (m, n multiples of 8 where they are the
+    // contiguous axis: vec), and every per-lane tile offset within 32 bits
+    if (TT_GEMM_DMA && vec && k % 32 == 0 && lda < (int64_t(1) << 22) && ldb < (int64_t(1) << 22)) {
+      const dim3 g2((unsigned)((n + 255) / 256), (unsigned)gy);
 #define TT_GEMM_D(TA, TB) \
   hipLaunchKernelGGL((k_gemm_dma<TA, TB>), g2, dim3(256), 0, s, (int)m, (int)n, (int)k, alpha, A, lda, B, ldb, beta, C)
       switch (transa * 2 + transb) {

@@ -57,8 +57,10 @@ def _run(capi, dt, ta, tb, m, n, k, alpha=1.0, beta=0.0, seed=0):
 SHAPES = [
     (1, 1, 1), (7, 5, 3), (128, 128, 64), (256, 128, 128), (129, 130, 65), (300, 257, 1000), (1000, 1, 37),
     (2, 3000, 17), (64, 64, 4096), (1024, 1024, 1024),
-    # full 128 x 256 tiles with k a multiple of 32 (the bf16 direct-to-LDS kernel)
+    # k a multiple of 32 (the bf16 direct-to-LDS kernel): full 128 x 256 tiles,
+    # then ragged m / n (multiples of 8, so every transpose combination runs it)
     (512, 768, 96), (128, 256, 32), (256, 512, 2048),
+    (136, 264, 96), (1000, 8, 64), (8, 1000, 32), (520, 776, 2048),
 ]
 
 
