@@ -269,6 +269,9 @@ __global__ __launch_bounds__(256, 2) void k_gemm(int M, int N, int K, float alph
 #ifndef TT_GEMM_DMA_S
 #define TT_GEMM_DMA_S 2
 #endif
+#ifndef TT_GEMM_DMA_GN
+#define TT_GEMM_DMA_GN 256  // C tile columns per workgroup (128: 91 VGPRs but 15-20 % slower)
+#endif
 
 // bf16 kernel for k % 32 == 0 with 16-byte aligned operands (ragged m and n
 // allowed): tiles go straight from global memory into LDS
@@ -330,7 +333,7 @@ __global__ __launch_bounds__(256, 3) void k_gemm_dma(int M, int N, int K, float 
                                                     int64_t lda, const u16* __restrict__ B, int64_t ldb,
                                                     float beta, u16* C) {
   using G = GemmT<u16>;
-  constexpr int GN = 256, NB = GN / 64, BK = 32, KS = BK / 16, S = TT_GEMM_DMA_S;
+  constexpr int GN = TT_GEMM_DMA_GN, NB = GN / 64, BK = 32, KS = BK / 16, S = TT_GEMM_DMA_S;
   using TileA = DmaTile<GM, !TA>;
   using TileB = DmaTile<GN, TB>;
   constexpr int PER = TileA::LOADS + TileB::LOADS;
@@ -419,7 +422,7 @@ int gemm_launch(const char* fn, int transa, int transb, int64_t m, int64_t n, in
     // k in whole steps, aligned rows (m, n multiples of 8 where they are the
     // contiguous axis: vec), and every per-lane tile offset within 32 bits
     if (TT_GEMM_DMA && vec && k % 32 == 0 && lda < (int64_t(1) << 22) && ldb < (int64_t(1) << 22)) {
-      const dim3 g2((unsigned)((n + 255) / 256), (unsigned)gy);
+      const dim3 g2((unsigned)((n + TT_GEMM_DMA_GN - 1) / TT_GEMM_DMA_GN), (unsigned)gy);
 #define TT_GEMM_D(TA, TB) \
   hipLaunchKernelGGL((k_gemm_dma<TA, TB>), g2, dim3(256), 0, s, (int)m, (int)n, (int)k, alpha, A, lda, B, ldb, beta, C)
       switch (transa * 2 + transb) {
