@@ -51,8 +51,6 @@ C4 = dict(B=64, H=32, Lkv=8192, d=128)
 MEASURED_TRAFFIC_MIB = {
     "attn_fwd": 580.7,
     "attn_bwd_delta": 264.0,
-    "attn_bwd_dkdv": 3072.4,   # includes the 2.06 GiB of dS it stores for the dQ GEMM
-    "attn_bwd_dq": 2369.0,     # the dQ GEMM: reads that dS back
     "attn_decode_split": 8209.1,
     "softmax_reg": 2048.1,
     "gemm_bf16_nn": 2527.8 + 149.6,  # k_gemm_dma 8192^3 NN (profiles/gemm_kernel_stats.md)     # k_softmax_reg<16>, 262144 x 1024 fp32 (profiles/softmax_rows_kernel_stats.md)
@@ -469,8 +467,7 @@ def main(argv=None):
             tf = kf[n] / (t * 1e-3) / 1e12 if kf[n] else None
             tb = traffic_bytes(n)
             kernels[n] = {"avg_ms": t, "tflops": tf, "frac": (tf / PEAK_BF16_TFLOPS) if tf else None,
-                          # measured HBM bytes per launch over this launch time: the dQ GEMM
-                          # (one GEMM unit over 2 GiB of stored dS) is bound by this, not MFMA
+                          # measured HBM bytes per launch over this launch time
                           "hbm_gbs": (tb / (t * 1e-3) / 1e9) if tb else None}
         out["kernels"] = kernels
         dom = max(per, key=per.get)

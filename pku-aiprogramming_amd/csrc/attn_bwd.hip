@@ -49,6 +49,9 @@ constexpr int bwd_nw(int D) { return D == 32 ? 4 : TT_BWD_WAVES; }
 constexpr int kBwdStages = TT_BWD_STAGES;
 static_assert(kBwdStages >= 2 && kBwdStages <= 4, "tile ring depth must be 2..4");
 constexpr int DQ_BN = 64;  // keys per LDS tile of the dQ kernel
+#ifndef TT_DQ_PIPE
+#define TT_DQ_PIPE 1
+#endif
 // Query rows per LDS tile of the dK/dV kernel: the ring of Q / dO tiles
 // plus the V rows of the workgroup fit 160 KB of LDS.
 #ifndef TT_DKDV_BQ128
@@ -105,16 +108,12 @@ __global__ __launch_bounds__(256) void attn_bwd_delta_kernel(const T* __restrict
 }
 
 // ------------------------------------------------------------------ bf16 dK, dV
-// MAT: also store dS for attn_bwd_dq_gemm_kernel, as one 2 KB image per
-// (32 keys, 32 queries) block (see ds_image_row); query tiles a wave skips
-// (all of its keys after all of the tile's queries) are stored as zeros.
-// Requires Lq, Lk multiples of the key tile.
-template <int D, bool CAUSAL, bool MAT>
+template <int D, bool CAUSAL>
 __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_bf16_kernel(
     const u16* __restrict__ Q, const u16* __restrict__ K, const u16* __restrict__ V,
     const u16* __restrict__ dO, const float* __restrict__ L2, const float* __restrict__ NDelta,
-    u16* __restrict__ dK, u16* __restrict__ dV, u16* __restrict__ dST, int Lq, int Lk, int BH, int nkt,
-    int group, float sl2, float scale) {
+    u16* __restrict__ dK, u16* __restrict__ dV, int Lq, int Lk, int BH, int nkt, int group, float sl2,
+    float scale) {
   using Tile = SwzTile<D>;
   constexpr int NW = bwd_nw(D), BN = 32 * NW, BQ = dkdv_bq(D), MT = BQ / 32, S = kBwdStages;
   constexpr int NC = D / 16, ND = D / 32;
@@ -124,7 +123,6 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_b
   constexpr int VS = 64;  // stride of the LSE / D row buffers (one 64-lane load each)
   using Dma = TileDma<D, BQ, NW>;
   constexpr int IPT = 2 * Dma::kLoads;  // Q + dO loads per wave per tile
-  constexpr int kStores = MAT ? 2 * MT : 0;  // dS image stores per wave per tile
   // One LDS block, carved at fixed byte offsets so that every operand read
   // is a per-lane address plus an immediate: the ring of Q / dO tiles with
   // their LSE (log2) / D rows and the workgroup's V rows, all filled by direct
@@ -165,20 +163,6 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_b
   // K operand of chunk c (each lane reads back only what it parked itself)
   uint32_t kofs = a0 + kOK + 16 * (64 * w + l);
   auto kop = [&](int c) { return c < KR ? kf[c] : lds_ld<bf16x8>(kofs + (c - KR) * NW * 1024); };
-  // dS image of (this wave's 32 keys, the 32 queries at q): this lane's 16
-  // accumulator values, 32 contiguous bytes at row ds_image_row(l) of image
-  // ((bh, q / 128, key / 32), (q / 32) % 4).  Stored non-temporal: the dQ
-  // GEMM reads it back from HBM.
-  u16* const dsimg = MAT ? dST + (((int64_t)bh * (Lq / 128)) * (Lk / 32) + key / 32) * 4096 + 16 * ds_image_row(l)
-                         : nullptr;
-  const int64_t img_row = (int64_t)(Lk / 32) * 4096;  // elements per 128 query rows of dS images
-  auto store_ds = [&](int q, const bf16x8 (&db)[2]) {
-    typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
-    const unsigned uq = q;  // q >= 0: unsigned division is a shift
-    u16* p = dsimg + (int64_t)(uq / 128) * img_row + (uq / 32 % 4) * 1024;
-    __builtin_nontemporal_store(__builtin_bit_cast(u32x4, db[0]), reinterpret_cast<u32x4*>(p));
-    __builtin_nontemporal_store(__builtin_bit_cast(u32x4, db[1]), reinterpret_cast<u32x4*>(p + 8));
-  };
   f32x16 adk[ND], adv[ND];
 #pragma unroll
   for (int dt = 0; dt < ND; ++dt) adk[dt] = adv[dt] = f32x16{};
@@ -275,7 +259,6 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_b
           db[r >> 3][r & 7] = (__bf16)(p * dp[r]);
         }
       }
-      if constexpr (MAT) store_ds(qb + 32 * mt, db);
       // dV^T += dO^T P and dK^T += Q^T dS over the 32 queries of this half:
       // k-chunk h holds queries 32mt + 16h + perm16 order.
       bf16x8 ov[2], oq[2];
@@ -300,26 +283,16 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_b
   // tile j at qb in ring buffer b (b < 0: j % S at run time)
   auto tile_at = [&](int qb, auto b_tag, auto mask_tag) __attribute__((always_inline)) {
     if constexpr (S == 2) {
-      // In flight: this tile's loads (issued after the previous tile's
-      // barrier), then the previous tile's dS stores.  Loads and stores retire
-      // in issue order, so the stores need not drain here.
-      wait_vmem_le<kStores>();
+      wait_vmem_le<0>();  // this tile's loads, issued after the previous tile's barrier
     } else if (wu == 0) {
-      wait_vmem_tiles<IPT + 2 + kStores, S - 1>(issued - 1 - j);
+      wait_vmem_tiles<IPT + 2, S - 1>(issued - 1 - j);
     } else {
-      wait_vmem_tiles<IPT + kStores, S - 1>(issued - 1 - j);
+      wait_vmem_tiles<IPT, S - 1>(issued - 1 - j);
     }
     __syncthreads();
     issue_next();
     if constexpr (CAUSAL && decltype(mask_tag)::value) {
-      if (qb + BQ - 1 < wk_lo) {  // every query of the tile precedes every key of the wave
-        if constexpr (MAT) {
-          const bf16x8 zero[2] = {bf16x8{}, bf16x8{}};
-#pragma unroll
-          for (int mt = 0; mt < MT; ++mt) store_ds(qb + 32 * mt, zero);
-        }
-        return;
-      }
+      if (qb + BQ - 1 < wk_lo) return;  // every query of the tile precedes every key of the wave
     }
     constexpr int bc = decltype(b_tag)::value;
     const int b = bc >= 0 ? bc : (unsigned)j % S;
@@ -541,129 +514,194 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dq_bf1
   }
 }
 
-// ------------------------------------------------------------------ bf16 dQ from stored dS
-// dQ = s dS K as one GEMM over the dS the dK/dV kernel stored, so dQ needs
-// no recompute of S and dP.  dS is stored as 2 KB images, one per (32 keys,
-// 32 queries) block, in [BH][Lq/128][Lk/32][4] order (the images one
-// workgroup reads form one contiguous stream): the dK/dV accumulator
-// registers as they are (lane l = key l % 32 of queries with g = l / 32;
-// register r = query 8(r/4) + 4g + r%4), row l at row ds_image_row(l).
-//
-// Workgroup = 4 waves x 32 queries = DQG_BM queries (one dK/dV key tile wide,
-// so every block it reads was written; above the diagonal as zeros).  Stages
-// of 32 keys (K rows, and the 4 dS images of the workgroup's queries, 8 KB
-// contiguous) stream through a TT_DQG_STAGES-deep LDS ring.  Per stage and
-// wave dQ^T (d x 32 queries) += K^T dS^T, both operands by LDS transpose
-// reads.  The dS operand puts query q(n) = 8(n%16 / 4) + 4(n / 16 % 2) + n % 4
-// of the wave's 32 in MFMA column n and keys in natural order (the K^T
-// operand reads its rows in the same order); output rows follow q(n).
-// Requires Lq, Lk multiples of DQG_BM.
-constexpr int DQG_BM = 128;
-constexpr int DQG_BN = 32;  // keys per stage
-// dS images are read once: loading them non-temporal keeps the K rows, which
-// every query tile of a head re-reads, in L2 (8 % less HBM fetch, same time).
-#ifndef TT_DQG_NT
-#define TT_DQG_NT 1
-#endif
-#ifndef TT_DQG_STAGES
-#define TT_DQG_STAGES 4
-#endif
-constexpr size_t kMaxDsBytes = size_t(8) << 30;  // largest dS workspace (bf16, Lq x Lk per head)
+// ------------------------------------------------------------------ bf16 dQ, software-pipelined (D = 64, 128)
+// Workgroup = 4 waves x 32 queries (lane = query, as the forward); blocks of
+// 32 keys (a K tile and a V tile) stream through a 4-deep LDS ring filled by
+// direct global->LDS loads.  Iteration n of a wave:
+//   MFMA  S^T_{n+1} = K_{n+1} Q^T,  dP^T_{n+1} = V_{n+1} dO^T        (next block)
+//   VALU  dS^T_n = 2^(s S^T_n log2(e) - LSE_n log2(e)) o (dP^T_n - D) (this block)
+//   MFMA  dQ^T += K_n^T dS^T_n                                         (this block)
+// so the exponentials of one block run on the VALU while the matrix cores
+// compute the next block's scores.  Barrier n makes tile n + 1 visible to
+// every wave and retires every read of tile n - 1, whose buffer then takes
+// tile n + 3: each tile gets two iterations of load lead.  The loop is
+// unrolled by the ring depth, so every LDS operand address is a
+// loop-invariant lane offset plus an immediate.
+constexpr int DQP_BN = 32;     // keys per block / LDS tile
+constexpr int DQP_STAGES = 4;  // LDS ring depth (the unrolled loop relies on it)
 
 template <int D, bool CAUSAL>
-__global__ __launch_bounds__(256, 2) void attn_bwd_dq_gemm_kernel(const u16* __restrict__ K,
-                                                                  const u16* __restrict__ dS,
-                                                                  u16* __restrict__ dQ, int Lq, int Lk, int BH,
-                                                                  int nqt, int group, float scale) {
-  constexpr int NW = 4, BM = DQG_BM, BN = DQG_BN, ND = D / 32, S = TT_DQG_STAGES;
-  static_assert(S >= 2 && S <= 4, "ring depth 2..4");
-  using KTile = SwzTile<D>;
-  constexpr int KE = KTile::kElems(BN), SE = (BM / 32) * 1024;  // elements per stage
-  using KDma = TileDma<D, BN, NW>;
-  constexpr int SL = SE / (NW * 512);  // dS load instructions per wave per stage (1 KB each)
-  constexpr int PER = KDma::kLoads + SL;
-  __shared__ __align__(16) u16 sK[S * KE];
-  __shared__ __align__(16) u16 sS[S * SE];
+__global__ __launch_bounds__(256, 2) void attn_bwd_dq_pipe_kernel(
+    const u16* __restrict__ Q, const u16* __restrict__ K, const u16* __restrict__ V,
+    const u16* __restrict__ dO, const float* __restrict__ L2, const float* __restrict__ NDelta,
+    u16* __restrict__ dQ, int Lq, int Lk, int BH, int nqt, int group, float sl2, float scale) {
+  using Tile = SwzTile<D>;
+  constexpr int NW = 4, BM = 32 * NW, BN = DQP_BN, S = DQP_STAGES;
+  constexpr int NC = D / 16, ND = D / 32;
+  constexpr int TE = Tile::kElems(BN);
+  using Dma = TileDma<D, BN, NW>;
+  constexpr int PER = 2 * Dma::kLoads;  // K + V load instructions per wave per tile
+  // ring buffer b: K tile at element 2 b TE, V tile at 2 b TE + TE
+  __shared__ __align__(16) u16 smem[2 * S * TE];
 
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int l = threadIdx.x & 63, g = l >> 5;
+  const int l = threadIdx.x & 63, g = l >> 5, r32 = l & 31;
   int qt, bh;
   map_tile(blockIdx.x, nqt, BH, group, qt, bh, CAUSAL);
-  const int q0 = qt * BM;
+  const int q0 = qt * BM, wq0 = q0 + 32 * w, qrow = wq0 + r32;
+  const int64_t qbase = (int64_t)bh * Lq * D;
   const int64_t kbase = (int64_t)bh * Lk * D;
-  // images of key block n and the workgroup's 4 query blocks: 8 KB at simg + 4096 n
-  const u16* simg = dS + ((int64_t)bh * (Lq / BM) + qt) * (Lk / 32) * 4096;
 
-  // Transpose reads: lane s of each 16-lane group points at row base + s / 4,
-  // 8-byte piece s % 4; the group then receives 4 consecutive rows of 16
-  // columns.  K^T operand of key chunk kc, half g: keys 16kc + 8g + (0..3)
-  // and 16kc + 8g + 4 + (0..3), d columns 32dt + 16G + (0..15).  dS operand:
-  // image rows 32G + the same keys, all 16 register columns.
-  const int t16 = l & 15, G = (l >> 4) & 1;
-  const int krow = 8 * g + (t16 >> 2), kcol = 16 * G + 4 * (t16 & 3);
-  const int srow = 32 * G + 8 * g, scol = 4 * (t16 & 3);
-
-  f32x16 acc[ND];
+  bf16x8 qf[NC], dof[NC];
+  {
+    const int qr = min(qrow, Lq - 1);  // padding rows read a valid row; never written back
 #pragma unroll
-  for (int dt = 0; dt < ND; ++dt) acc[dt] = f32x16{};
-
-  const int ntiles = (CAUSAL ? min(Lk, q0 + BM) : Lk) / BN;
-  KDma kdma;
-  kdma.init();
-  int issued = 0;
-  auto issue_next = [&]() {
-    if (issued < ntiles) {
-      const int b = issued % S;
-      kdma.issue(K + kbase, BN * issued, Lk, sK + b * KE);
-      const u16* src = simg + (int64_t)issued * 4096;
-      const uint32_t lds = lds_addr(sS + b * SE);
+    for (int c = 0; c < NC; ++c) {
+      qf[c] = __builtin_bit_cast(bf16x8, ldg16(Q + qbase + (int64_t)qr * D + 16 * c + 8 * g));
+      dof[c] = __builtin_bit_cast(bf16x8, ldg16(dO + qbase + (int64_t)qr * D + 16 * c + 8 * g));
+    }
+  }
+  // padding query rows: P = 2^(s - inf) = 0
+  const float lse2 = qrow < Lq ? L2[(int64_t)bh * Lq + qrow] : INFINITY;
+  const float ndl = qrow < Lq ? NDelta[(int64_t)bh * Lq + qrow] : 0.f;
+  f32x16 adq[ND];
 #pragma unroll
-      for (int i = 0; i < SL; ++i) {
-        const uint32_t off = 1024u * (uint32_t)(i * NW + w);
-#if TT_DQG_NT
-        glds16_nt(src, off + 16u * (uint32_t)l, lds + off);
-#else
-        glds16(src, off + 16u * (uint32_t)l, lds + off);
-#endif
+  for (int dt = 0; dt < ND; ++dt) adq[dt] = f32x16{};
+
+  const int kend = CAUSAL ? min(Lk, q0 + BM) : Lk;  // >= 1
+  const int ntiles = (kend + BN - 1) / BN;
+  // Last block this wave computes: its diagonal block (causal) or the last
+  // one.  Every earlier block lies inside Lk and before every query of the
+  // wave; the last one is always computed with the mask.
+  const int last = CAUSAL ? min(wq0 / BN, ntiles - 1) : ntiles - 1;
+
+  // Loop-invariant LDS element offsets of this lane: K / V row operands of
+  // k-chunk c (16-byte chunk 2c + g of key row r32), and the transpose reads
+  // of the K^T operand of d-tile dt (rows trow, trow + 8; key chunk h adds
+  // 16 rows, which keeps the swizzle).
+  int kidx[NC], tidx[2][ND];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) kidx[c] = Tile::chunk(r32, 2 * c + g);
+  {
+    const int t16 = l & 15;
+    const int trow = 4 * g + (t16 >> 2), tcol = 16 * ((l >> 4) & 1) + 4 * (t16 & 3);
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt) {
+      tidx[0][dt] = Tile::at4(trow, 32 * dt + tcol);
+      tidx[1][dt] = Tile::at4(trow + 8, 32 * dt + tcol);
+    }
+  }
+
+  // S^T and dP^T of the block in ring buffer B
+  auto sdp = [&](auto b_tag, f32x16& s, f32x16& dp) __attribute__((always_inline)) {
+    constexpr int B = decltype(b_tag)::value;
+    const u16* tK = smem + 2 * B * TE;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const bf16x8 ka = *reinterpret_cast<const bf16x8*>(&tK[kidx[c]]);
+      const bf16x8 va = *reinterpret_cast<const bf16x8*>(&tK[TE + kidx[c]]);
+      s = mfma_bf16_32x32x16(ka, qf[c], c == 0 ? f32x16{} : s);
+      dp = mfma_bf16_32x32x16(va, dof[c], c == 0 ? f32x16{} : dp);
+    }
+  };
+  // dS^T of the block at keys kb in ring buffer B, then dQ^T += K^T dS^T
+  auto dsq = [&](auto b_tag, const f32x16& s, const f32x16& dp, int kb, auto mask_tag)
+                 __attribute__((always_inline)) {
+    constexpr int B = decltype(b_tag)::value;
+    constexpr bool MASK = decltype(mask_tag)::value;
+    bf16x8 db[2];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      float p = fast_exp2(fmaf(s[r], sl2, -lse2));
+      if constexpr (MASK) {
+        const int key = kb + acc_row(r, g);
+        if (key >= Lk || (CAUSAL && key > qrow)) p = 0.f;
       }
+      db[r >> 3][r & 7] = (__bf16)(p * (dp[r] + ndl));
+    }
+    const u16* tK = smem + 2 * B * TE;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int dt = 0; dt < ND; ++dt) {
+        const bf16x8 a = lds_read_tr16x2(&tK[tidx[0][dt] + 16 * h * D], &tK[tidx[1][dt] + 16 * h * D]);
+        adq[dt] = mfma_bf16_32x32x16(a, db[h], adq[dt]);
+      }
+  };
+
+  Dma dma;
+  dma.init();
+  int issued = 0;
+  auto issue_tile = [&](int n) {  // tile n into ring buffer n % S (n < ntiles)
+    u16* dst = smem + 2 * (n % S) * TE;
+    dma.issue(K + kbase, BN * n, Lk, dst);
+    dma.issue(V + kbase, BN * n, Lk, dst + TE);
+  };
+  // Barrier n: this wave's loads of tile n + 1 have landed (loads retire in
+  // issue order), then every wave's are visible and tile n - 1 is retired;
+  // tile n + S - 1 goes into its buffer.
+  auto barrier_n = [&](int n) __attribute__((always_inline)) {
+    const int ahead = issued - n - 2;
+    wait_vmem_tiles<PER, S - 2>(ahead > 0 ? ahead : 0);
+    __syncthreads();
+    if (n + S - 1 < ntiles) {
+      issue_tile(n + S - 1);
       ++issued;
     }
   };
-  for (int s0 = 0; s0 < S - 1; ++s0) issue_next();
-  for (int n = 0; n < ntiles; ++n) {
-    wait_vmem_tiles<PER>(issued - 1 - n);  // tiles n + 1 .. issued - 1 may stay in flight
-    __syncthreads();
-    issue_next();
-    const u16* tK = sK + (n % S) * KE;
-    const u16* tS = sS + (n % S) * SE + w * 1024;  // this wave's query block
-#pragma unroll
-    for (int kc = 0; kc < BN / 16; ++kc) {
-      const int sr = srow + 16 * kc;  // a multiple of 4; rows sr .. sr + 3 and sr + 4 .. sr + 7
-      const bf16x8 b = lds_read_tr16x2(&tS[16 * (ds_image_row(sr) + (t16 >> 2)) + scol],
-                                       &tS[16 * (ds_image_row(sr + 4) + (t16 >> 2)) + scol]);
-#pragma unroll
-      for (int dt = 0; dt < ND; ++dt) {
-        const int r0 = 16 * kc + krow;
-        const bf16x8 a =
-            lds_read_tr16x2(&tK[KTile::at4(r0, 32 * dt + kcol)], &tK[KTile::at4(r0 + 4, 32 * dt + kcol)]);
-        acc[dt] = mfma_bf16_32x32x16(a, b, acc[dt]);
-      }
-    }
+
+  for (; issued < S - 1 && issued < ntiles; ++issued) issue_tile(issued);
+  wait_vmem_le<0>();  // also retires the Q / dO / LSE / D loads before the loop
+  __syncthreads();
+
+  using B0 = std::integral_constant<int, 0>;
+  using B1 = std::integral_constant<int, 1>;
+  using B2 = std::integral_constant<int, 2>;
+  using B3 = std::integral_constant<int, 3>;
+  f32x16 sA, pA, sB, pB;
+  sdp(B0{}, sA, pA);
+  // iteration n with a next block (n < last): buffer n % 4 = B
+  auto it = [&](int n, auto b_tag, f32x16& sc, f32x16& pc, f32x16& sn, f32x16& pn) __attribute__((always_inline)) {
+    constexpr int B = decltype(b_tag)::value;
+    barrier_n(n);
+    sdp(std::integral_constant<int, (B + 1) % 4>{}, sn, pn);
+    dsq(b_tag, sc, pc, BN * n, std::false_type{});
+  };
+  int n = 0;
+  for (; n + 4 <= last; n += 4) {
+    it(n, B0{}, sA, pA, sB, pB);
+    it(n + 1, B1{}, sB, pB, sA, pA);
+    it(n + 2, B2{}, sA, pA, sB, pB);
+    it(n + 3, B3{}, sB, pB, sA, pA);
   }
+  const int rem = last - n;  // 0..3 iterations with a next block, then the last block
+  if (rem >= 1) it(n, B0{}, sA, pA, sB, pB);
+  if (rem >= 2) it(n + 1, B1{}, sB, pB, sA, pA);
+  if (rem >= 3) it(n + 2, B2{}, sA, pA, sB, pB);
+  barrier_n(last);
+  switch (rem) {
+    case 0: dsq(B0{}, sA, pA, BN * last, std::true_type{}); break;
+    case 1: dsq(B1{}, sB, pB, BN * last, std::true_type{}); break;
+    case 2: dsq(B2{}, sA, pA, BN * last, std::true_type{}); break;
+    default: dsq(B3{}, sB, pB, BN * last, std::true_type{}); break;
+  }
+  // later tiles belong to other waves of the workgroup: take part in their
+  // barriers and loads
+  for (int m = last + 1; m < ntiles; ++m) barrier_n(m);
   wait_vmem_le<0>();  // nothing may be in flight into LDS when the workgroup exits
 
-  const int n = l & 31;
-  const int q = q0 + 32 * w + 8 * ((n & 15) >> 2) + 4 * ((n >> 4) & 1) + (n & 3);
-  u16* row = dQ + ((int64_t)bh * Lq + q) * D;
+  if (qrow < Lq) {
+    u16* row = dQ + qbase + (int64_t)qrow * D;
 #pragma unroll
-  for (int dt = 0; dt < ND; ++dt)
+    for (int dt = 0; dt < ND; ++dt)
 #pragma unroll
-    for (int r = 0; r < 16; r += 4) {
-      uint2 v;
-      v.x = pack_bf16x2(acc[dt][r] * scale, acc[dt][r + 1] * scale);
-      v.y = pack_bf16x2(acc[dt][r + 2] * scale, acc[dt][r + 3] * scale);
-      *reinterpret_cast<uint2*>(row + 32 * dt + acc_row(r, g)) = v;
-    }
+      for (int r = 0; r < 16; r += 4) {
+        uint2 v;
+        v.x = pack_bf16x2(adq[dt][r] * scale, adq[dt][r + 1] * scale);
+        v.y = pack_bf16x2(adq[dt][r + 2] * scale, adq[dt][r + 3] * scale);
+        *reinterpret_cast<uint2*>(row + 32 * dt + acc_row(r, g)) = v;
+      }
+  }
 }
 
 // ------------------------------------------------------------------ launchers
@@ -692,33 +730,18 @@ static int launch_bwd(const T* q, const T* k, const T* v, const T* o, const floa
     if (nkt * BH > 0x7fffffff || nqt * BH > 0x7fffffff) return fail(TT_ERR_ARG, "attention backward: grid too large");
     // heads in flight per XCD: tiles for the resident workgroups of its 32 CUs
     const int gk = pick_group(BH, nkt, 32 * 8 / NW), gq = pick_group(BH, nqt, 32 * 8 / NW);
-    // dQ: one GEMM over the stored dS when the tiles are full and the dS
-    // workspace stays under kMaxDsBytes; otherwise recompute S and dP.
-    if constexpr (D >= 64) {
-      const size_t ds_bytes = (size_t)BH * (size_t)Lk * (size_t)Lq * sizeof(u16);
-      const bool mat = (32 * NW) % DQG_BM == 0 && Lq % DQG_BM == 0 && Lk % (32 * NW) == 0 &&
-                       Lq <= (int64_t(1) << 24) && ds_bytes <= kMaxDsBytes;
-      if (mat) {
-        u16* ds = nullptr;
-        if ((rc = workspace(2, ds_bytes, (void**)&ds))) return rc;
-        hipLaunchKernelGGL((attn_bwd_dkdv_bf16_kernel<D, CAUSAL, true>), dim3((unsigned)(nkt * BH)), dim3(64 * NW),
-                           0, st, q, k, v, dout, l2, delta, dk, dv, ds, (int)Lq, (int)Lk, (int)BH, (int)nkt, gk, sl2,
-                           scale);
-        TT_LAUNCHED("attention backward dK/dV launch", st);
-        const int64_t nqg = Lq / DQG_BM;
-        const int gg = pick_group(BH, nqg, 32 * 2);
-        hipLaunchKernelGGL((attn_bwd_dq_gemm_kernel<D, CAUSAL>), dim3((unsigned)(nqg * BH)), dim3(256), 0, st, k, ds,
-                           dq, (int)Lq, (int)Lk, (int)BH, (int)nqg, gg, scale);
-        TT_LAUNCHED("attention backward dQ launch", st);
-        return ok();
-      }
-    }
-    hipLaunchKernelGGL((attn_bwd_dkdv_bf16_kernel<D, CAUSAL, false>), dim3((unsigned)(nkt * BH)), dim3(64 * NW), 0,
-                       st, q, k, v, dout, l2, delta, dk, dv, nullptr, (int)Lq, (int)Lk, (int)BH, (int)nkt, gk, sl2,
-                       scale);
+    hipLaunchKernelGGL((attn_bwd_dkdv_bf16_kernel<D, CAUSAL>), dim3((unsigned)(nkt * BH)), dim3(64 * NW), 0, st, q,
+                       k, v, dout, l2, delta, dk, dv, (int)Lq, (int)Lk, (int)BH, (int)nkt, gk, sl2, scale);
     TT_LAUNCHED("attention backward dK/dV launch", st);
-    hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<D, CAUSAL>), dim3((unsigned)(nqt * BH)), dim3(64 * NW), 0, st,
-                       q, k, v, dout, l2, delta, dq, (int)Lq, (int)Lk, (int)BH, (int)nqt, gq, sl2, scale);
+    if constexpr (D >= 64 && TT_DQ_PIPE) {
+      const int64_t nqp = (Lq + 127) / 128;
+      const int gp = pick_group(BH, nqp, 32 * 2);
+      hipLaunchKernelGGL((attn_bwd_dq_pipe_kernel<D, CAUSAL>), dim3((unsigned)(nqp * BH)), dim3(256), 0, st, q, k, v,
+                         dout, l2, delta, dq, (int)Lq, (int)Lk, (int)BH, (int)nqp, gp, sl2, scale);
+    } else {
+      hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<D, CAUSAL>), dim3((unsigned)(nqt * BH)), dim3(64 * NW), 0, st,
+                         q, k, v, dout, l2, delta, dq, (int)Lq, (int)Lk, (int)BH, (int)nqt, gq, sl2, scale);
+    }
     TT_LAUNCHED("attention backward dQ launch", st);
   } else {
     const int64_t nkt = (Lk + BWD_F32_BN - 1) / BWD_F32_BN;

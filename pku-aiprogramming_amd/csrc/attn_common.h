@@ -192,12 +192,6 @@ __device__ __forceinline__ void glds16(const void* sbase, uint32_t voff, uint32_
   asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds)
                : "memory", "m0");
 }
-// Same, marked non-temporal: data read once (streamed), kept out of the way
-// of data that is reused from L2.
-__device__ __forceinline__ void glds16_nt(const void* sbase, uint32_t voff, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1 nt" ::"v"(voff), "s"(sbase), "s"(lds)
-               : "memory", "m0");
-}
 __device__ __forceinline__ void glds4(const void* sbase, uint32_t voff, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(sbase), "s"(lds)
                : "memory", "m0");
@@ -267,13 +261,6 @@ struct TileDma {
     }
   }
 };
-
-// Row position of row l (0..63) of a 2 KB dS image (64 rows of 32 bytes):
-// bit 2 flipped in rows 8..15 of every 16, so that the four 4-row groups a
-// transpose read touches (rows 0-3, 8-11, 32-35, 40-43 plus a multiple of
-// 4) spread over both halves of the LDS banks.  An involution that keeps
-// groups of 4 consecutive rows (starting at a multiple of 4) together.
-__device__ __forceinline__ constexpr int ds_image_row(int l) { return l ^ (((l >> 3) & 1) << 2); }
 
 // s_waitcnt vmcnt(N): wait until at most N of this wave's global loads are
 // outstanding (loads retire in order), LDS / export counters untouched.

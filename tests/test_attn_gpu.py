@@ -201,7 +201,7 @@ def test_c4_bf16_decode(capi):
 
 def test_long_sequence_few_heads_bf16(capi):
     """L = 8192 with only two heads (B*H not a multiple of 8: no per-XCD head
-    grouping; 64 query tiles per head; a 128 MiB stored-dS workspace): one
+    grouping; 64 query tiles per head): one
     head against the float64 oracle, both through the identities."""
     B, H, L, d = 1, 2, 8192, 128
     _say("long sequence: bf16 causal B=1 H=2 L=8192 d=128")
@@ -273,8 +273,7 @@ SHAPES = [
     (1, 1, 65, 300, 128, False),
     (2, 2, 257, 257, 32, True),
     (1, 1, 3, 1000, 64, False),
-    # d = 128 with Lq, Lk multiples of 128: the stored-dS backward (dQ as a
-    # GEMM over the dS images the dK / dV kernel writes)
+    # d = 128 with Lq, Lk multiples of the 128-row tiles: no masked edge tile
     (1, 2, 256, 256, 128, True),
     (2, 1, 512, 512, 128, True),
     (1, 1, 128, 512, 128, False),
