@@ -59,9 +59,22 @@ int tt_init(int device);
 /* The library stream as an opaque handle (hipStream_t). */
 void* tt_stream(void);
 
+/* Caller streams (no counterpart in the reference, which launches on the
+ * default stream and synchronises after every launch): a new non-blocking
+ * stream of default priority, a wait for all work queued on a stream (NULL:
+ * the library stream), and its destruction (after waiting for it and
+ * releasing the library's per-stream scratch buffers).  Every launcher takes
+ * such a stream; two calls on different streams share no scratch memory. */
+int tt_stream_create(void** stream);
+int tt_stream_sync(void* stream);
+int tt_stream_destroy(void* stream);
+
 /* Caching device allocator (hipMalloc-backed).
  * Replaces cudaMalloc at src/Tinytensor.cu:21,39,60,77,116,252,375.
- * Blocks are reused by size class; tt_empty_cache() returns them to HIP. */
+ * Blocks are reused by size class; tt_empty_cache() returns them (and the
+ * launchers' scratch buffers) to HIP.  A refused allocation is TT_ERR_NOMEM;
+ * with TT_FAIL_ALLOC_AFTER=n in the environment, the process's device
+ * allocations n, n+1, ... are refused (failure injection for tests). */
 int tt_malloc(void** ptr, size_t bytes);
 /* Replaces cudaFree at src/Tinytensor.cu:90,108,239,378.  NULL is a no-op. */
 int tt_free(void* ptr);
@@ -163,12 +176,10 @@ int tt_attn_fwd_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v, ui
  * through MatMul.gradient (:421-429), Transpose.gradient (:338-340),
  * MulScalar.gradient (:241-242), EWiseDiv.gradient (:296-298),
  * BroadcastTo/Summation.gradient (:373-380, :400-408), Exp.gradient (:469-470).
- * Uses a library-owned scratch buffer of 2*B*H*Lq floats (-D and LSE*log2(e)).
- * The bf16 entry point, for d in {64, 128} with Lq and Lk multiples of 128,
- * also stores dS (bf16, B*H*Lq*Lk elements, at most 8 GiB) in a library-owned
- * workspace and computes dQ = s dS K from it as one GEMM; other shapes
- * recompute S and dP for dQ.  Results agree either way (dS enters the dQ
- * MFMA as bf16 in both). */
+ * No L x L matrix is stored: one kernel owns dK/dV rows (keys) and one owns
+ * dQ rows (queries), and each recomputes S and dP from Q, K, V, dO and the
+ * LSE.  Uses a library-owned scratch buffer of 2*B*H*Lq floats (-D and
+ * LSE*log2(e)), one per stream. */
 int tt_attn_bwd_f32(const float* q, const float* k, const float* v, const float* o,
                     const float* lse, const float* do_, float* dq, float* dk, float* dv,
                     int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t d,

@@ -711,7 +711,8 @@ static int launch_bwd(const T* q, const T* k, const T* v, const T* o, const floa
   constexpr bool BF = sizeof(T) == 2;
   // workspace: -D (negated row sums of dO o O) and LSE * log2(e), fp32 [B*H*Lq] each
   float* delta = nullptr;
-  int rc = workspace(0, (size_t)(2 * BH * Lq) * sizeof(float), (void**)&delta);
+  WorkspaceLease ws;  // held until the kernels that read the buffer are launched
+  int rc = ws.get(st, kWsBackwardRows, (size_t)(2 * BH * Lq) * sizeof(float), (void**)&delta);
   if (rc) return rc;
   const int64_t rows = BH * Lq;
   float* l2 = delta + rows;

@@ -197,7 +197,8 @@ static int launch_decode(const T* q, const T* k, const T* v, T* o, float* lse, i
   if (BH * nsplit > 0x7fffffff) return fail(TT_ERR_ARG, "attention decode: grid too large");
   void* ws = nullptr;
   const size_t need = (size_t)(BH * nsplit) * (D + 1) * sizeof(float);
-  int rc = workspace(1, need, &ws);
+  WorkspaceLease lease;  // held until both kernels are launched
+  int rc = lease.get(st, kWsDecodePartials, need, &ws);
   if (rc) return rc;
   float* part_o = (float*)ws;
   float* part_lse = part_o + BH * nsplit * D;

@@ -26,11 +26,23 @@ int ensure_init();
 // kernel launch on `s`; a no-op unless instrumentation is enabled.
 void after_launch(hipStream_t s);
 
-// Device scratch owned by the library, grown on demand and kept for reuse.
-// `slot` separates independent users (0: attention bwd row sums,
-// 1: decode partials).  Stream-ordered on the library stream; callers that
-// pass another stream must not overlap two calls that share a slot.
-int workspace(int slot, size_t bytes, void** ptr);
+// Device scratch of the attention launchers: one buffer per (stream, user),
+// grown on demand and kept for reuse.  A lease holds the workspace lock from
+// get() until it is destroyed: keep it alive until every kernel that reads
+// the buffer has been launched on that stream.
+enum { kWsBackwardRows = 0, kWsDecodePartials = 1 };
+class WorkspaceLease {
+ public:
+  WorkspaceLease();
+  ~WorkspaceLease();
+  WorkspaceLease(const WorkspaceLease&) = delete;
+  WorkspaceLease& operator=(const WorkspaceLease&) = delete;
+  int get(hipStream_t stream, int user, size_t bytes, void** ptr);
+
+ private:
+  struct Impl;
+  Impl* impl_;
+};
 
 }  // namespace tt
 

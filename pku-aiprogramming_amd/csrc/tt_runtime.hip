@@ -15,6 +15,7 @@
 #include <unordered_map>
 #include <vector>
 
+#include "device_cache.h"
 #include "tt_internal.h"
 
 namespace tt {
@@ -51,57 +52,33 @@ hipStream_t stream_or_default(void* s) {
 }
 
 // ---------------------------------------------------------------- allocator
-// Size classes: 512 B granules below 1 MiB, 2 MiB granules above.  Freed
-// blocks go to a multimap keyed by class size and are reused first-fit
-// (smallest class >= request, at most 2x the request to bound waste).
-struct Alloc {
-  std::multimap<size_t, void*> free_blocks;
-  std::unordered_map<void*, size_t> live;  // ptr -> class size
-  size_t in_use = 0, cached = 0;
-};
-static Alloc g_alloc;
-
-static size_t size_class(size_t bytes) {
-  if (bytes == 0) bytes = 1;
-  const size_t small = 512, big = size_t(2) << 20;
-  if (bytes < (size_t(1) << 20)) return (bytes + small - 1) / small * small;
-  return (bytes + big - 1) / big * big;
-}
-
-static int alloc_block(size_t bytes, void** ptr) {
-  size_t cls = size_class(bytes);
-  {
-    std::lock_guard<std::mutex> lk(g_mu);
-    auto it = g_alloc.free_blocks.lower_bound(cls);
-    if (it != g_alloc.free_blocks.end() && it->first <= 2 * cls) {
-      *ptr = it->second;
-      size_t c = it->first;
-      g_alloc.free_blocks.erase(it);
-      g_alloc.live[*ptr] = c;
-      g_alloc.cached -= c;
-      g_alloc.in_use += c;
-      return TT_OK;
-    }
-  }
-  void* p = nullptr;
-  hipError_t e = hipMalloc(&p, cls);
-  if (e != hipSuccess) {
-    // Return cached blocks to HIP and retry once.
-    (void)hipGetLastError();
-    tt_empty_cache();
-    e = hipMalloc(&p, cls);
+// hipMalloc / hipFree / hipStreamSynchronize as the backend of the caching
+// allocator and the workspace cache (device_cache.h).  Allocation failures,
+// real or injected by TT_FAIL_ALLOC_AFTER, are TT_ERR_NOMEM with a message.
+struct HipBackend {
+  AllocFailureInjector inject;
+  int alloc(size_t bytes, void** p) {
+    if (inject.next_fails())
+      return fail(TT_ERR_NOMEM, "tt_malloc: allocation of " + std::to_string(bytes) +
+                                    " bytes refused (TT_FAIL_ALLOC_AFTER failure injection)");
+    const hipError_t e = hipMalloc(p, bytes);
     if (e != hipSuccess) {
       (void)hipGetLastError();
-      return fail(TT_ERR_NOMEM, "tt_malloc: hipMalloc of " + std::to_string(cls) +
-                                    " bytes failed: " + hipGetErrorString(e));
+      return fail(TT_ERR_NOMEM,
+                  "tt_malloc: hipMalloc of " + std::to_string(bytes) + " bytes failed: " + hipGetErrorString(e));
     }
+    return TT_OK;
   }
-  std::lock_guard<std::mutex> lk(g_mu);
-  g_alloc.live[p] = cls;
-  g_alloc.in_use += cls;
-  *ptr = p;
-  return TT_OK;
-}
+  // hipFree waits for the device work that may still use the block
+  void release(void* p) { (void)hipFree(p); }
+  int sync(void* stream) {
+    const hipError_t e = hipStreamSynchronize(static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? TT_OK : hip_fail(e, "hipStreamSynchronize (workspace)");
+  }
+};
+static HipBackend g_backend;
+static BlockCache<HipBackend> g_blocks(g_backend);
+static WorkspaceCache<HipBackend> g_ws(g_backend, g_blocks);
 
 // ---------------------------------------------------------------- instrumentation
 static std::vector<void*> g_launch_events;
@@ -113,27 +90,13 @@ void after_launch(hipStream_t s) {
 }
 
 // ---------------------------------------------------------------- workspace
-static void* g_ws[4] = {nullptr, nullptr, nullptr, nullptr};
-static size_t g_ws_bytes[4] = {0, 0, 0, 0};
-
-int workspace(int slot, size_t bytes, void** ptr) {
-  if (slot < 0 || slot >= 4) return fail(TT_ERR_ARG, "workspace: bad slot");
-  if (bytes <= g_ws_bytes[slot] && g_ws[slot]) {
-    *ptr = g_ws[slot];
-    return TT_OK;
-  }
-  if (g_ws[slot]) {
-    // The old buffer may still be read by queued work on the stream.
-    TT_HIP(hipStreamSynchronize(g_stream));
-    tt_free(g_ws[slot]);
-    g_ws[slot] = nullptr;
-    g_ws_bytes[slot] = 0;
-  }
-  int rc = alloc_block(bytes, &g_ws[slot]);
-  if (rc) return rc;
-  g_ws_bytes[slot] = bytes;
-  *ptr = g_ws[slot];
-  return TT_OK;
+struct WorkspaceLease::Impl {
+  WorkspaceCache<HipBackend>::Lease lease{g_ws};
+};
+WorkspaceLease::WorkspaceLease() : impl_(new Impl) {}
+WorkspaceLease::~WorkspaceLease() { delete impl_; }
+int WorkspaceLease::get(hipStream_t s, int user, size_t bytes, void** ptr) {
+  return impl_->lease.get(static_cast<void*>(s), user, bytes, ptr);
 }
 
 // ---------------------------------------------------------------- elementwise
@@ -291,48 +254,62 @@ void* tt_stream(void) {
   return (void*)g_stream;
 }
 
+int tt_stream_create(void** stream) {
+  if (!stream) return fail(TT_ERR_ARG, "tt_stream_create: null pointer");
+  *stream = nullptr;
+  int rc = ensure_init();
+  if (rc) return rc;
+  hipStream_t s;
+  // Default priority on purpose, like the library stream.
+  TT_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+  *stream = (void*)s;
+  return ok();
+}
+
+int tt_stream_sync(void* stream) {
+  int rc = ensure_init();
+  if (rc) return rc;
+  TT_HIP(hipStreamSynchronize(stream_or_default(stream)));
+  return ok();
+}
+
+int tt_stream_destroy(void* stream) {
+  if (!stream) return TT_OK;
+  if (stream == (void*)g_stream) return fail(TT_ERR_ARG, "tt_stream_destroy: the library stream is not the caller's");
+  const int rc = g_ws.release_stream(stream);  // waits for the stream
+  if (rc) return rc;
+  TT_HIP(hipStreamDestroy(static_cast<hipStream_t>(stream)));
+  return ok();
+}
+
 int tt_malloc(void** ptr, size_t bytes) {
   if (!ptr) return fail(TT_ERR_ARG, "tt_malloc: null pointer");
   *ptr = nullptr;
   int rc = ensure_init();
   if (rc) return rc;
-  rc = alloc_block(bytes, ptr);
+  rc = g_blocks.alloc(bytes, ptr);
   if (rc) return rc;
   return ok();
 }
 
 int tt_free(void* ptr) {
   if (!ptr) return TT_OK;
-  std::lock_guard<std::mutex> lk(g_mu);
-  auto it = g_alloc.live.find(ptr);
-  if (it == g_alloc.live.end()) return fail(TT_ERR_ARG, "tt_free: pointer not from tt_malloc");
-  size_t c = it->second;
-  g_alloc.live.erase(it);
-  g_alloc.in_use -= c;
   // Work queued on the library stream that still reads this block runs
   // before any later user of the block on the same stream.
-  g_alloc.free_blocks.emplace(c, ptr);
-  g_alloc.cached += c;
+  if (!g_blocks.release(ptr)) return fail(TT_ERR_ARG, "tt_free: pointer not from tt_malloc");
   return TT_OK;
 }
 
 int tt_empty_cache(void) {
-  std::multimap<size_t, void*> blocks;
-  {
-    std::lock_guard<std::mutex> lk(g_mu);
-    blocks.swap(g_alloc.free_blocks);
-    g_alloc.cached = 0;
-  }
   if (!g_inited) return TT_OK;
-  if (!blocks.empty()) TT_HIP(hipStreamSynchronize(g_stream));
-  for (auto& kv : blocks) TT_HIP(hipFree(kv.second));
-  return TT_OK;
+  TT_HIP(hipStreamSynchronize(g_stream));
+  const int rc = g_ws.release_all();
+  g_blocks.trim();
+  return rc ? rc : ok();
 }
 
 int tt_mem_stats(size_t* in_use, size_t* cached) {
-  std::lock_guard<std::mutex> lk(g_mu);
-  if (in_use) *in_use = g_alloc.in_use;
-  if (cached) *cached = g_alloc.cached;
+  g_blocks.stats(in_use, cached);
   return TT_OK;
 }
 

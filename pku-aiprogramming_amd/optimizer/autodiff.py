@@ -1,58 +1,68 @@
 """Reverse-mode differentiation over the ``Value`` graph.
 
-Follows the reference driver (Task3/Tinytensor/optimizer/autodiff.py:9-61):
-a post-order DFS gives a topological order; the output is seeded with
-``out_grad``; nodes are visited in reverse order, each node's gradient
-contributions are summed in the order they were produced (first + second +
-...), stored in ``node.grad`` and pushed through ``op.gradient_as_tuple`` to
-the inputs.
+Same entry points and results as the reference driver
+(Task3/Tinytensor/optimizer/autodiff.py:9-61): ``find_topo_sort`` returns the
+nodes inputs-first, and ``compute_gradient_of_variables(output, out_grad)``
+leaves in every node's ``.grad`` the gradient of sum(output * out_grad).
 
-The DFS is iterative here, so deep graphs need no recursion-limit change
-(the reference raises the limit to 10**8 at :7 instead).
+The order is found by Kahn's algorithm on user counts instead of a recursive
+depth-first search, so graphs of any depth need no recursion limit: a node
+is processed once every node that uses it has pushed its contribution, and
+contributions are added up in the order they arrive.
 """
 from __future__ import annotations
 
+from collections import deque
 from typing import Dict, List
 
 from basic_operator import Value
 
 
-def find_topo_sort(node_list: List[Value]) -> List[Value]:
-    """Topological order (inputs before users) of the graph ending at
-    ``node_list``: post-order DFS along input edges."""
-    visited = set()
+def _users_first(outputs: List[Value]) -> List[Value]:
+    """Every node reachable from `outputs`, each after all of its users."""
+    users: Dict[Value, int] = {}
+    stack = []
+    for root in outputs:
+        if root not in users:
+            users[root] = 0
+            stack.append(root)
+    while stack:  # count the edges into each reachable node
+        node = stack.pop()
+        for inp in node.inputs:
+            if inp in users:
+                users[inp] += 1
+            else:
+                users[inp] = 1
+                stack.append(inp)
+    ready = deque(n for n in dict.fromkeys(outputs) if users[n] == 0)
     order: List[Value] = []
-    for root in node_list:
-        if root in visited:
-            continue
-        visited.add(root)
-        stack = [(root, iter(root.inputs))]
-        while stack:
-            node, it = stack[-1]
-            nxt = next(it, None)
-            if nxt is None:
-                stack.pop()
-                order.append(node)
-            elif nxt not in visited:
-                visited.add(nxt)
-                stack.append((nxt, iter(nxt.inputs)))
+    while ready:
+        node = ready.popleft()
+        order.append(node)
+        for inp in node.inputs:
+            users[inp] -= 1
+            if users[inp] == 0:
+                ready.append(inp)
     return order
 
 
+def find_topo_sort(node_list: List[Value]) -> List[Value]:
+    """Topological order of the graph ending at `node_list`: every node comes
+    after all of its inputs."""
+    return _users_first(node_list)[::-1]
+
+
 def compute_gradient_of_variables(output_tensor: Value, out_grad: Value) -> None:
-    """Set ``.grad`` on every node that ``output_tensor`` depends on, for the
-    upstream gradient ``out_grad`` (i.e. the gradient of
-    sum(output * out_grad))."""
-    contributions: Dict[Value, List[Value]] = {output_tensor: [out_grad]}
-    for node in reversed(find_topo_sort([output_tensor])):
-        parts = contributions.get(node)
-        if not parts:
+    """Set ``.grad`` on `output_tensor` and every node it depends on, for the
+    upstream gradient `out_grad` (the gradient of sum(output * out_grad))."""
+    pending: Dict[Value, Value] = {output_tensor: out_grad}
+    for node in _users_first([output_tensor]):
+        grad = pending.pop(node, None)
+        if grad is None:
             continue
-        total = parts[0]
-        for extra in parts[1:]:
-            total = total + extra
-        node.grad = total
+        node.grad = grad
         if node.op is None:
             continue
-        for inp, g in zip(node.inputs, node.op.gradient_as_tuple(total, node)):
-            contributions.setdefault(inp, []).append(g)
+        for inp, part in zip(node.inputs, node.op.gradient_as_tuple(grad, node)):
+            prev = pending.get(inp)
+            pending[inp] = part if prev is None else prev + part

@@ -1,58 +1,41 @@
-"""Device handle of the Python layer (Task3/Tinytensor/optimizer/device.py:9-59).
+"""Device handle of the TinyTensor Python layer.
 
-Graph data lives in numpy arrays on the host; GPU ops move it to the MI355X
-through ``myTensor`` inside ``compute``/``gradient``.  ``Tensor.device``
-therefore always reports ``cpu()``, as in the reference.
+Graph data of the Python layer always lives in host numpy arrays; the GPU
+operators move it to the MI355X inside their forward / gradient and bring the
+result back.  So the only device a graph node reports is the host, and the
+only part of the reference's device module its callers use is that handle:
+``cpu()``, compared by value and usable as a dict key
+(reference: Task3/Tinytensor/optimizer/device.py:9-59, used by
+optimizer/operators.py:8,40-58).
 """
-import numpy as np
+from __future__ import annotations
 
 
 class Device:
-    """Base class."""
+    """A named place where a node's data lives; equal when the names are."""
+
+    __slots__ = ("name",)
+
+    def __init__(self, name: str):
+        self.name = name
+
+    def __repr__(self) -> str:
+        return f"{self.name}()"
+
+    def __eq__(self, other) -> bool:
+        return isinstance(other, Device) and other.name == self.name
+
+    def __hash__(self) -> int:
+        return hash(("Device", self.name))
+
+    def enabled(self) -> bool:
+        """Whether node data can be held here (only the host can)."""
+        return self.name == "cpu"
 
 
-class CPUDevice(Device):
-    def __repr__(self):
-        return "cpu()"
-
-    def __hash__(self):
-        return hash(repr(self))
-
-    def __eq__(self, other):
-        return isinstance(other, CPUDevice)
-
-    def enabled(self):
-        return True
-
-    def zeros(self, *shape, dtype="float32"):
-        return np.zeros(shape, dtype=dtype)
-
-    def ones(self, *shape, dtype="float32"):
-        return np.ones(shape, dtype=dtype)
-
-    def randn(self, *shape):
-        return np.random.randn(*shape)
-
-    def rand(self, *shape):
-        return np.random.rand(*shape)
-
-    def one_hot(self, n, i, dtype="float32"):
-        return np.eye(n, dtype=dtype)[i]
-
-    def empty(self, shape, dtype="float32"):
-        return np.empty(shape, dtype=dtype)
-
-    def full(self, shape, fill_value, dtype="float32"):
-        return np.full(shape, fill_value, dtype=dtype)
+_HOST = Device("cpu")
 
 
-def cpu():
-    return CPUDevice()
-
-
-def default_device():
-    return cpu()
-
-
-def all_devices():
-    return [cpu()]
+def cpu() -> Device:
+    """The host device: where every node's numpy data lives."""
+    return _HOST

@@ -1,151 +1,153 @@
-"""Tensor and operators of the TinyTensor Python layer, with the fused
-MI355X attention op.
+"""``Tensor`` and the operators of the TinyTensor Python layer, with the fused
+MI355X attention operator.
 
 Drop-in for Task3/Tinytensor/optimizer/operators.py on the attention path:
+callers keep ``from operators import *``, build ``Tensor`` from numpy arrays,
+other ``Tensor`` objects or ``myTensor`` tensors, compose with ``@ + - * / **``
+and the op functions, call ``.backward(out_grad)`` and read ``.grad``
+(reference :14-187 for ``Tensor``, :194-475 for the numpy ops, :478-491 for
+``ReLU``).
 
-* ``Tensor(Value)`` with the same constructors (numpy array, ``Tensor``, or a
-  ``myTensor`` tensor; :17-58), ``backward(out_grad)`` (:115-119) and the
-  operator sugar (:133-187);
-* the numpy ops the reference composes attention from -- ``EWiseAdd``,
-  ``AddScalar``, ``EWiseMul``, ``MulScalar``, ``PowerScalar``, ``EWisePow``,
-  ``EWiseDiv``, ``DivScalar``, ``Transpose``, ``Reshape``, ``BroadcastTo``,
-  ``Summation``, ``MatMul``, ``Negate``, ``Log``, ``Exp`` (:194-475) -- with
-  the same forward semantics and gradient rules;
-* ``ReLU`` over ``myTensor`` (:478-491);
-* new: ``Attention(TensorOp)`` -- one fused GPU op for
-  ``softmax(Q K^T * scale + mask) V`` in fp32 or bf16, shaped like ``FC``
-  (:498-532): ``compute`` uploads with ``Tensor_*(..., "gpu")``, calls
-  ``myLayer.AttentionForward`` and stashes the device tensors and the
-  log-sum-exp; ``gradient`` calls ``myLayer.AttentionBackward``.
+Design:
 
-GPU ops return float32 numpy arrays through ``numpy()`` (one copy); the
-reference returns float64 arrays built from a Python list.
+* the elementwise operators are rows of one rule table (``_RULES``): a
+  forward on arrays and a vector-Jacobian product written with graph ops, so
+  gradients of gradients stay expressible; ``EWiseAdd``, ``MulScalar``, ... are
+  classes generated from it, so ``isinstance`` checks and constructor
+  arguments (the scalar of the ``*Scalar`` ops) work as before;
+* shape operators (``Transpose``, ``Reshape``, ``BroadcastTo``, ``Summation``)
+  and ``MatMul`` reduce a broadcast gradient back to the input's shape by one
+  helper, ``_unbroadcast``;
+* the GPU operators run through ``myTensor`` / ``myLayer`` (the pybind11 drop-in
+  over the HIP C-ABI).  ``Attention`` keeps the device tensors of its forward
+  on the output node (``node.saved``), releases them after its gradient, and
+  recomputes them from the node's inputs when a second backward needs them.
 
-The MNIST layers of the reference (FC, Conv, MaxPool and the softmax losses,
+Deliberate departures from the reference: ``matmul(a, b)`` propagates
+gradients (the reference's wraps its arguments in new leaves, :432-433), and
+``c - t`` computes c - t (the reference aliases ``__rsub__`` to ``__sub__``,
+:187).  The reference's MNIST layers (FC, Conv, MaxPool, the softmax losses,
 :494-665) are not part of this build.
 """
 from __future__ import annotations
 
 import math
-from typing import List, Optional, Tuple
+from typing import Callable, Optional, Sequence
 
 import numpy as np
 
 from autodiff import compute_gradient_of_variables
 from basic_operator import Op, Value
 from device import Device, cpu
-import myLayer as ml  # noqa: E402  (compiled extension; import fails loudly if unbuilt)
-from myTensor import Tensor_bf16 as tb
-from myTensor import Tensor_float as tf
-from myTensor import Tensor_int as ti
+import myLayer as ml  # compiled extension: the import fails loudly when it is not built
+from myTensor import Tensor_bf16, Tensor_float, Tensor_int
 
-_MYTENSOR_TYPES = (tf, ti, tb)
+_DEVICE_TENSORS = (Tensor_float, Tensor_int, Tensor_bf16)
+
+
+def _host_array(obj, dtype=None) -> np.ndarray:
+    """A fresh host array for a Tensor's data from numpy-like input, another
+    Tensor or a myTensor tensor (downloaded once)."""
+    if isinstance(obj, Tensor):
+        obj = obj.realize_cached_data()
+    elif isinstance(obj, _DEVICE_TENSORS):
+        obj = obj.numpy()
+    return np.array(obj, dtype=dtype)
 
 
 class Tensor(Value):
+    """A graph node whose data is a host numpy array."""
+
     grad: "Tensor"
 
     def __init__(self, array, *, device: Optional[Device] = None, dtype=None, requires_grad=True, **kwargs):
-        if isinstance(array, Tensor):
-            device = device or array.device
-            dtype = dtype or array.dtype
-            if device == array.device and dtype == array.dtype:
-                data = array.realize_cached_data()
-            else:
-                data = Tensor._array_from_numpy(array.numpy(), device=device, dtype=dtype)
-        elif isinstance(array, _MYTENSOR_TYPES):
-            data = Tensor._array_from_mytensor(array, device=device or cpu(), dtype=dtype)
+        if device is not None and device != cpu():
+            raise ValueError(f"Tensor data lives on the host; device {device!r} is not available")
+        if isinstance(array, Tensor) and dtype is None:
+            data = array.realize_cached_data()  # shares the array, as the reference does
         else:
-            data = Tensor._array_from_numpy(np.asarray(array), device=device or cpu(), dtype=dtype)
-        self._init(None, [], cached_data=data, requires_grad=requires_grad)
+            data = _host_array(array, dtype)
+        self._setup(None, (), data, requires_grad)
 
-    @staticmethod
-    def _array_from_numpy(numpy_array, device, dtype):
-        return np.array(numpy_array, dtype=dtype)
-
-    @staticmethod
-    def _array_from_mytensor(mytensor, device, dtype):
-        return np.array(mytensor.numpy(), dtype=dtype)
-
-    @staticmethod
-    def make_from_op(op: Op, inputs: List["Value"]):
-        t = Tensor.__new__(Tensor)
-        t._init(op, inputs)
-        if not t.requires_grad:
-            return t.detach()
-        t.realize_cached_data()
-        return t
-
-    @staticmethod
-    def make_const(data, requires_grad=False):
-        t = Tensor.__new__(Tensor)
-        if isinstance(data, Tensor):
-            data = data.realize_cached_data()
-        t._init(None, [], cached_data=data, requires_grad=requires_grad)
-        return t
-
+    # ---------------------------------------------------------------- data
     @property
-    def data(self):
+    def data(self) -> "Tensor":
         return self.detach()
 
     @data.setter
-    def data(self, value):
-        assert isinstance(value, Tensor)
-        assert value.dtype == self.dtype, f"{value.dtype} {self.dtype}"
+    def data(self, value: "Tensor") -> None:
+        if not isinstance(value, Tensor):
+            raise TypeError("Tensor.data takes a Tensor")
+        if value.dtype != self.dtype:
+            raise TypeError(f"Tensor.data: dtype {value.dtype} does not match {self.dtype}")
         self.cached_data = value.realize_cached_data()
 
-    def detach(self):
+    def detach(self) -> "Tensor":
         return Tensor.make_const(self.realize_cached_data())
 
     @property
     def shape(self):
-        if isinstance(self.cached_data, tuple):
-            return [1]
         return self.realize_cached_data().shape
 
     @property
     def dtype(self):
-        if isinstance(self.cached_data, tuple):
-            return float
         return self.realize_cached_data().dtype
 
     @property
-    def device(self):
+    def device(self) -> Device:
         return cpu()
 
-    def backward(self, out_grad=None):
+    def numpy(self) -> np.ndarray:
+        return self.realize_cached_data()
+
+    def backward(self, out_grad=None) -> None:
+        """Gradients of sum(self * out_grad) into .grad of every node this
+        one depends on; out_grad defaults to ones."""
         if out_grad is None:
-            out_grad = Tensor(np.ones(self.shape, dtype=self.dtype), dtype=self.dtype, requires_grad=False)
+            out_grad = Tensor(np.ones(self.shape, dtype=self.dtype), requires_grad=False)
         elif not isinstance(out_grad, Tensor):
             out_grad = Tensor(out_grad, requires_grad=False)
         compute_gradient_of_variables(self, out_grad)
 
-    def __repr__(self):
-        return "Tensor(" + str(self.realize_cached_data()) + ")"
+    def __repr__(self) -> str:
+        return f"Tensor({self.realize_cached_data()})"
 
-    def __str__(self):
+    def __str__(self) -> str:
         return str(self.realize_cached_data())
 
-    def numpy(self):
-        return self.realize_cached_data()
-
+    # ------------------------------------------------------------ operators
     def __add__(self, other):
         return EWiseAdd()(self, other) if isinstance(other, Tensor) else AddScalar(other)(self)
-
-    def __mul__(self, other):
-        return EWiseMul()(self, other) if isinstance(other, Tensor) else MulScalar(other)(self)
-
-    def __pow__(self, other):
-        return EWisePow()(self, other) if isinstance(other, Tensor) else PowerScalar(other)(self)
 
     def __sub__(self, other):
         return EWiseAdd()(self, Negate()(other)) if isinstance(other, Tensor) else AddScalar(-other)(self)
 
+    def __rsub__(self, other):
+        return AddScalar(other)(Negate()(self))
+
+    def __mul__(self, other):
+        return EWiseMul()(self, other) if isinstance(other, Tensor) else MulScalar(other)(self)
+
     def __truediv__(self, other):
         return EWiseDiv()(self, other) if isinstance(other, Tensor) else DivScalar(other)(self)
 
+    def __rtruediv__(self, other):
+        return MulScalar(other)(PowerScalar(-1)(self))
+
+    def __pow__(self, other):
+        return EWisePow()(self, other) if isinstance(other, Tensor) else PowerScalar(other)(self)
+
+    def __neg__(self):
+        return Negate()(self)
+
     def __matmul__(self, other):
         return MatMul()(self, other)
+
+    def __rmatmul__(self, other):
+        return MatMul()(other, self)
+
+    __radd__ = __add__
+    __rmul__ = __mul__
 
     def matmul(self, other):
         return MatMul()(self, other)
@@ -159,299 +161,261 @@ class Tensor(Value):
     def reshape(self, shape):
         return Reshape(shape)(self)
 
-    def __neg__(self):
-        return Negate()(self)
-
     def transpose(self, axes=None):
         return Transpose(axes)(self)
 
-    __radd__ = __add__
-    __rmul__ = __mul__
-    __rsub__ = __sub__
-    __rmatmul__ = __matmul__
-
 
 class TensorOp(Op):
+    """An operator whose nodes are Tensors."""
+
     def __call__(self, *args):
         return Tensor.make_from_op(self, args)
 
 
-# --------------------------------------------------------------- elementwise
+def _const(array) -> Tensor:
+    return Tensor.make_const(array)
 
-class EWiseAdd(TensorOp):
-    def compute(self, a, b):
-        return a + b
+
+# ------------------------------------------------------------------ elementwise rule table
+# name -> (number of tensor inputs, takes a scalar, forward(arrays, c), vjp(g, node, c))
+# The vjp returns one gradient per tensor input, built from graph ops.
+def _inputs(node):
+    return node.inputs
+
+
+_RULES = {
+    "EWiseAdd": (2, False, lambda x, c: x[0] + x[1], lambda g, n, c: (g, g)),
+    "AddScalar": (1, True, lambda x, c: x[0] + c, lambda g, n, c: (g,)),
+    "EWiseMul": (2, False, lambda x, c: x[0] * x[1],
+                 lambda g, n, c: (g * _inputs(n)[1], g * _inputs(n)[0])),
+    "MulScalar": (1, True, lambda x, c: x[0] * c, lambda g, n, c: (g * c,)),
+    "PowerScalar": (1, True, lambda x, c: np.power(x[0], c),
+                    lambda g, n, c: (g * (_inputs(n)[0] ** (c - 1)) * c,)),
+    "EWisePow": (2, False, lambda x, c: np.power(x[0], x[1]),
+                 lambda g, n, c: (g * _inputs(n)[1] * _inputs(n)[0] ** (_inputs(n)[1] - 1),
+                                  g * n.detach() * Log()(_inputs(n)[0]))),
+    "EWiseDiv": (2, False, lambda x, c: x[0] / x[1],
+                 lambda g, n, c: (g / _inputs(n)[1], -(g * _inputs(n)[0]) / (_inputs(n)[1] ** 2))),
+    "DivScalar": (1, True, lambda x, c: x[0] / c, lambda g, n, c: (g / c,)),
+    "Negate": (1, False, lambda x, c: -x[0], lambda g, n, c: (-g,)),
+    "Log": (1, False, lambda x, c: np.log(x[0]), lambda g, n, c: (g / _inputs(n)[0],)),
+    # d exp(a) = exp(a) da, with exp(a) the node's own (constant) output
+    "Exp": (1, False, lambda x, c: np.exp(x[0]), lambda g, n, c: (g * n.detach(),)),
+}
+
+
+class _Elementwise(TensorOp):
+    """Operator defined by a row of the rule table."""
+
+    _arity = 1
+    _forward: Callable = None
+    _vjp: Callable = None
+    _scalar_op = False
+
+    def __init__(self, scalar=None):
+        if self._scalar_op and scalar is None:
+            raise TypeError(f"{type(self).__name__} needs a scalar")
+        self.scalar = scalar
+
+    def __call__(self, *args):
+        if len(args) != self._arity:
+            raise TypeError(f"{type(self).__name__} takes {self._arity} tensor input(s), got {len(args)}")
+        return Tensor.make_from_op(self, args)
+
+    def compute(self, *arrays):
+        return type(self)._forward(arrays, self.scalar)
 
     def gradient(self, out_grad, node):
-        return out_grad, out_grad
+        return type(self)._vjp(out_grad, node, self.scalar)
+
+
+def _make_elementwise(name, rule):
+    arity, scalar, fwd, vjp = rule
+    return type(name, (_Elementwise,), {
+        "_arity": arity, "_scalar_op": scalar, "_forward": staticmethod(fwd), "_vjp": staticmethod(vjp),
+        "__doc__": f"Elementwise operator {name} (rule table row).", "__module__": __name__,
+    })
+
+
+EWiseAdd = _make_elementwise("EWiseAdd", _RULES["EWiseAdd"])
+AddScalar = _make_elementwise("AddScalar", _RULES["AddScalar"])
+EWiseMul = _make_elementwise("EWiseMul", _RULES["EWiseMul"])
+MulScalar = _make_elementwise("MulScalar", _RULES["MulScalar"])
+PowerScalar = _make_elementwise("PowerScalar", _RULES["PowerScalar"])
+EWisePow = _make_elementwise("EWisePow", _RULES["EWisePow"])
+EWiseDiv = _make_elementwise("EWiseDiv", _RULES["EWiseDiv"])
+DivScalar = _make_elementwise("DivScalar", _RULES["DivScalar"])
+Negate = _make_elementwise("Negate", _RULES["Negate"])
+Log = _make_elementwise("Log", _RULES["Log"])
+Exp = _make_elementwise("Exp", _RULES["Exp"])
 
 
 def add(a, b):
     return EWiseAdd()(a, b)
 
 
-class AddScalar(TensorOp):
-    def __init__(self, scalar):
-        self.scalar = scalar
-
-    def compute(self, a):
-        return a + self.scalar
-
-    def gradient(self, out_grad, node):
-        return out_grad
-
-
 def add_scalar(a, scalar):
     return AddScalar(scalar)(a)
-
-
-class EWiseMul(TensorOp):
-    def compute(self, a, b):
-        return a * b
-
-    def gradient(self, out_grad, node):
-        a, b = node.inputs
-        return out_grad * b, out_grad * a
 
 
 def multiply(a, b):
     return EWiseMul()(a, b)
 
 
-class MulScalar(TensorOp):
-    def __init__(self, scalar):
-        self.scalar = scalar
-
-    def compute(self, a):
-        return a * self.scalar
-
-    def gradient(self, out_grad, node):
-        return out_grad * self.scalar
-
-
 def mul_scalar(a, scalar):
     return MulScalar(scalar)(a)
-
-
-class PowerScalar(TensorOp):
-    """a ** scalar, elementwise."""
-
-    def __init__(self, scalar):
-        self.scalar = scalar
-
-    def compute(self, a):
-        return np.power(a, self.scalar)
-
-    def gradient(self, out_grad, node):
-        a = node.inputs[0]
-        return out_grad * self.scalar * (a ** (self.scalar - 1))
 
 
 def power_scalar(a, scalar):
     return PowerScalar(scalar)(a)
 
 
-class EWisePow(TensorOp):
-    """a ** b, elementwise."""
-
-    def compute(self, a, b):
-        return a ** b
-
-    def gradient(self, out_grad, node):
-        a, b = node.inputs
-        if not isinstance(a, Tensor) or not isinstance(b, Tensor):
-            raise ValueError("Both inputs must be tensors.")
-        return out_grad * b * (a ** (b - 1)), out_grad * (a ** b) * log(a)
-
-
 def power(a, b):
     return EWisePow()(a, b)
-
-
-class EWiseDiv(TensorOp):
-    """a / b; d/da = 1/b, d/db = -a/b^2 (quotient rule, as the reference)."""
-
-    def compute(self, a, b):
-        return a / b
-
-    def gradient(self, out_grad, node):
-        a, b = node.inputs
-        return out_grad / b, -out_grad * a / (b ** 2)
 
 
 def divide(a, b):
     return EWiseDiv()(a, b)
 
 
-class DivScalar(TensorOp):
-    def __init__(self, scalar):
-        self.scalar = scalar
-
-    def compute(self, a):
-        return a / self.scalar
-
-    def gradient(self, out_grad, node):
-        return out_grad / self.scalar
-
-
 def divide_scalar(a, scalar):
     return DivScalar(scalar)(a)
-
-
-class Negate(TensorOp):
-    def compute(self, a):
-        return -a
-
-    def gradient(self, out_grad, node):
-        return -out_grad
 
 
 def negate(a):
     return Negate()(a)
 
 
-class Log(TensorOp):
-    def compute(self, a):
-        return np.log(a)
-
-    def gradient(self, out_grad, node):
-        return out_grad / node.inputs[0]
-
-
 def log(a):
     return Log()(a)
-
-
-class Exp(TensorOp):
-    def compute(self, a):
-        return np.exp(a)
-
-    def gradient(self, out_grad, node):
-        # the reference multiplies by a constant exp(input), not by a graph node
-        return out_grad * np.exp(node.inputs[0].realize_cached_data())
 
 
 def exp(a):
     return Exp()(a)
 
 
-# --------------------------------------------------------------- shape ops
+# ------------------------------------------------------------------ shapes and products
+
+def _unbroadcast(grad: Tensor, shape: Sequence[int]) -> Tensor:
+    """Sum `grad` down to `shape`: over the leading axes it has beyond
+    len(shape), and over the axes where `shape` has size 1 and grad does not
+    (numpy broadcasting in reverse)."""
+    shape = tuple(shape)
+    gshape = tuple(grad.shape)
+    lead = len(gshape) - len(shape)
+    axes = tuple(range(lead)) + tuple(lead + i for i, s in enumerate(shape) if s == 1 and gshape[lead + i] != 1)
+    if axes:
+        grad = Summation(axes)(grad)
+    if tuple(grad.shape) != shape:
+        grad = Reshape(shape)(grad)
+    return grad
+
 
 class Transpose(TensorOp):
-    """Swap two axes; default: the last two (reference :323-336)."""
+    """Swap two axes: the given pair, or the last two (reference :323-340)."""
 
     def __init__(self, axes: Optional[tuple] = None):
         self.axes = axes
 
-    def _perm(self, ndim):
-        perm = list(range(ndim))
-        if self.axes is None:
-            perm[-2], perm[-1] = perm[-1], perm[-2]
-        else:
-            x, y = self.axes
-            perm[x], perm[y] = perm[y], perm[x]
-        return perm
-
     def compute(self, a):
-        return np.transpose(a, self._perm(a.ndim))
+        i, j = self.axes if self.axes is not None else (-2, -1)
+        return np.swapaxes(a, i, j)
 
     def gradient(self, out_grad, node):
-        return transpose(out_grad, self.axes)
-
-
-def transpose(a, axes=None):
-    return Transpose(axes)(a)
+        return Transpose(self.axes)(out_grad)
 
 
 class Reshape(TensorOp):
     def __init__(self, shape):
-        self.shape = shape
+        self.shape = tuple(shape)
 
     def compute(self, a):
         return np.reshape(a, self.shape)
 
     def gradient(self, out_grad, node):
-        return reshape(out_grad, node.inputs[0].shape)
-
-
-def reshape(a, shape):
-    return Reshape(shape)(a)
+        return Reshape(node.inputs[0].shape)(out_grad)
 
 
 class BroadcastTo(TensorOp):
     def __init__(self, shape):
-        self.shape = shape
+        self.shape = tuple(shape)
 
     def compute(self, a):
         return np.broadcast_to(a, self.shape)
 
     def gradient(self, out_grad, node):
-        in_shape = tuple(node.inputs[0].shape)
-        padded = (1,) * (len(self.shape) - len(in_shape)) + in_shape
-        axes = tuple(i for i, (s, p) in enumerate(zip(self.shape, padded)) if s != p)
-        return (reshape(summation(out_grad, axes=axes), in_shape),)
-
-
-def broadcast_to(a, shape):
-    return BroadcastTo(shape)(a)
+        return _unbroadcast(out_grad, node.inputs[0].shape)
 
 
 class Summation(TensorOp):
-    def __init__(self, axes: Optional[tuple] = None):
+    """Sum over `axes` (an int, a tuple, or None for all), dropping them."""
+
+    def __init__(self, axes=None):
         self.axes = axes
 
+    def _axes(self, ndim):
+        if self.axes is None:
+            return tuple(range(ndim))
+        ax = self.axes if isinstance(self.axes, (tuple, list)) else (self.axes,)
+        return tuple(a % ndim for a in ax)
+
     def compute(self, a):
-        return np.sum(a) if self.axes is None else np.sum(a, axis=self.axes)
+        return np.sum(a, axis=self._axes(a.ndim))
 
     def gradient(self, out_grad, node):
-        in_shape = node.inputs[0].shape
-        if self.axes is None:
-            axes = tuple(range(len(in_shape)))
-        elif isinstance(self.axes, (list, tuple)):
-            axes = tuple(self.axes)
-        else:
-            axes = (self.axes,)
-        kept = [1 if i in axes else s for i, s in enumerate(in_shape)]
-        return broadcast_to(reshape(out_grad, kept), in_shape)
-
-
-def summation(a, axes=None):
-    return Summation(axes)(a)
+        in_shape = tuple(node.inputs[0].shape)
+        axes = self._axes(len(in_shape))
+        kept = tuple(1 if i in axes else s for i, s in enumerate(in_shape))
+        return BroadcastTo(in_shape)(Reshape(kept)(out_grad))
 
 
 class MatMul(TensorOp):
-    """np.matmul with batch broadcasting; gradients sum over broadcast
-    leading axes (reference :416-429)."""
+    """np.matmul with broadcast batch axes; each gradient is summed back to
+    its input's shape (reference :416-429)."""
 
     def compute(self, a, b):
         return np.matmul(a, b)
 
     def gradient(self, out_grad, node):
         a, b = node.inputs
-        ga = out_grad @ transpose(b)
-        gb = transpose(a) @ out_grad
-        if len(ga.shape) > len(a.shape):
-            ga = summation(ga, axes=tuple(range(len(ga.shape) - len(a.shape))))
-        if len(gb.shape) > len(b.shape):
-            gb = summation(gb, axes=tuple(range(len(gb.shape) - len(b.shape))))
-        return ga, gb
+        ga = MatMul()(out_grad, Transpose()(b)) if len(b.shape) > 1 else None
+        gb = MatMul()(Transpose()(a), out_grad) if len(a.shape) > 1 else None
+        if ga is None or gb is None:
+            raise NotImplementedError("MatMul gradient needs operands of rank >= 2")
+        return _unbroadcast(ga, a.shape), _unbroadcast(gb, b.shape)
+
+
+def transpose(a, axes=None):
+    return Transpose(axes)(a)
+
+
+def reshape(a, shape):
+    return Reshape(shape)(a)
+
+
+def broadcast_to(a, shape):
+    return BroadcastTo(shape)(a)
+
+
+def summation(a, axes=None):
+    return Summation(axes)(a)
 
 
 def matmul(a, b):
-    # As in the reference (:432-433) this wraps both arguments in new leaf
-    # tensors, so it does not propagate gradients; use ``a @ b`` for that.
-    return MatMul()(Tensor(a), Tensor(b))
+    return MatMul()(a, b)
 
 
-# --------------------------------------------------------------- GPU ops
+# ------------------------------------------------------------------ GPU operators
 
 class ReLU(TensorOp):
+    """max(x, 0) on the GPU through myTensor (reference :478-491)."""
+
     def compute(self, a):
-        return tf(np.asarray(a, np.float32), "gpu").ReluForward().numpy()
+        return Tensor_float(np.asarray(a, np.float32), "gpu").ReluForward().numpy()
 
     def gradient(self, out_grad, node):
-        x = tf(np.asarray(node.inputs[0].realize_cached_data(), np.float32), "gpu")
-        g = tf(np.asarray(out_grad.realize_cached_data(), np.float32), "gpu")
+        x = Tensor_float(np.asarray(node.inputs[0].realize_cached_data(), np.float32), "gpu")
+        g = Tensor_float(np.asarray(out_grad.realize_cached_data(), np.float32), "gpu")
         return Tensor(x.ReluBackward(g))
 
 
@@ -459,57 +423,66 @@ def relu(a):
     return ReLU()(a)
 
 
+_ATTN_DTYPES = {"float32": Tensor_float, "bf16": Tensor_bf16}
+
+
+def _default_scale(d: int) -> float:
+    return float(np.float32(1.0 / math.sqrt(d)))
+
+
 class Attention(TensorOp):
     """Fused scaled dot-product attention on the MI355X.
 
-    ``compute(q, k, v)`` -> ``softmax(q @ k^T * scale + mask) @ v`` with
-    q [B, H, Lq, d], k/v [B, H, Lk, d], d in {32, 64, 128}; ``mask`` is -inf
-    where key > query when ``causal``.  ``scale`` defaults to 1/sqrt(d)
-    rounded to float32.  ``dtype`` "float32" runs the fp32 kernels, "bf16"
-    rounds the inputs to bfloat16 on upload and accumulates in fp32.
-
-    The same result as composing the reference's ops
-    ``(q @ k.transpose()) * scale`` -> ``+ mask`` -> ``exp`` / ``sum`` /
-    ``divide`` -> ``@ v`` (operators.py:163-164, 234-239, 194-196, 611-612,
-    416-419), without materialising the L x L scores; ``gradient`` returns
-    (dQ, dK, dV) for the upstream gradient like that composition's backward.
+    ``softmax(q @ k^T * scale + mask) @ v`` for q [B, H, Lq, d] and k, v
+    [B, H, Lk, d], d in {32, 64, 128}; the mask is -inf where key > query when
+    ``causal``.  ``scale`` defaults to 1/sqrt(d) rounded to float32.  dtype
+    "float32" runs the fp32 kernels; "bf16" rounds the inputs to bfloat16 on
+    upload and accumulates in fp32.  The result equals the reference's
+    composition ``(q @ k.transpose()) * scale`` -> ``+ mask`` -> exp / sum /
+    divide -> ``@ v`` (operators.py:163-164, 234-239, 194-196, 611-612,
+    416-419) without forming the L x L scores, and ``gradient`` returns
+    (dQ, dK, dV) like that composition's backward.  A ``myLayer`` call runs
+    each direction (bind_Layer.cpp:12-23 style, shaped like FC at
+    operators.py:498-532).
     """
 
     def __init__(self, causal: bool = False, scale: Optional[float] = None, dtype: str = "float32"):
-        if dtype not in ("float32", "bf16"):
-            raise ValueError("Attention dtype must be 'float32' or 'bf16'")
+        if dtype not in _ATTN_DTYPES:
+            raise ValueError(f"Attention dtype must be one of {sorted(_ATTN_DTYPES)}, got {dtype!r}")
         self.causal = bool(causal)
         self.scale = scale
         self.dtype = dtype
-        self._saved = None
 
-    def _cls(self):
-        return tb if self.dtype == "bf16" else tf
-
-    def _scale_for(self, d):
-        return float(np.float32(1.0 / math.sqrt(d))) if self.scale is None else float(self.scale)
+    def _run_forward(self, q, k, v):
+        """Upload, run the forward kernel; returns the device tensors
+        (q, k, v, out, lse) and the scale used."""
+        T = _ATTN_DTYPES[self.dtype]
+        qd, kd, vd = (T(np.asarray(x, np.float32), "gpu") for x in (q, k, v))
+        out, lse = T([1], "gpu"), Tensor_float([1], "gpu")
+        scale = _default_scale(qd.get_shape()[-1]) if self.scale is None else float(self.scale)
+        ml.AttentionForward(qd, kd, vd, out, lse, scale, self.causal)
+        return (qd, kd, vd, out, lse), scale
 
     def compute(self, q, k, v):
-        T = self._cls()
-        qt = T(np.asarray(q, np.float32), "gpu")
-        kt = T(np.asarray(k, np.float32), "gpu")
-        vt = T(np.asarray(v, np.float32), "gpu")
-        out = T([1], "gpu")
-        lse = tf([1], "gpu")
-        ml.AttentionForward(qt, kt, vt, out, lse, self._scale_for(qt.get_shape()[-1]), self.causal)
-        self._saved = (qt, kt, vt, out, lse)
+        (_, _, _, out, _), _ = self._run_forward(q, k, v)
         return out.numpy()
 
+    def forward(self, node, q, k, v):
+        dev, scale = self._run_forward(q, k, v)
+        node.saved = (dev, scale)
+        return dev[3].numpy()
+
     def gradient(self, out_grad, node):
-        T = self._cls()
-        if self._saved is None:
-            self.compute(*[x.realize_cached_data() for x in node.inputs])
-        qt, kt, vt, out, lse = self._saved
+        saved = node.saved
+        if saved is None:  # a second backward through this node: recompute the forward
+            saved = self._run_forward(*[x.realize_cached_data() for x in node.inputs])
+        (qd, kd, vd, out, lse), scale = saved
+        node.saved = None  # release the device tensors
+        T = _ATTN_DTYPES[self.dtype]
         go = T(np.asarray(out_grad.realize_cached_data(), np.float32), "gpu")
         gq, gk, gv = T([1], "gpu"), T([1], "gpu"), T([1], "gpu")
-        ml.AttentionBackward(qt, kt, vt, out, lse, go, gq, gk, gv, self._scale_for(qt.get_shape()[-1]),
-                             self.causal)
-        return Tensor(gq), Tensor(gk), Tensor(gv)
+        ml.AttentionBackward(qd, kd, vd, out, lse, go, gq, gk, gv, scale, self.causal)
+        return Tensor(gq, requires_grad=False), Tensor(gk, requires_grad=False), Tensor(gv, requires_grad=False)
 
 
 def attention(q, k, v, causal: bool = False, scale: Optional[float] = None, dtype: str = "float32"):
@@ -518,23 +491,20 @@ def attention(q, k, v, causal: bool = False, scale: Optional[float] = None, dtyp
 
 class AttentionDecode(TensorOp):
     """Single-query decode (forward only): q [B, H, 1, d] against a K/V cache
-    [B, H, Lkv, d]; memory-bound split-KV kernel."""
+    [B, H, Lkv, d], no mask; the memory-bound split-KV kernel."""
 
     def __init__(self, scale: Optional[float] = None, dtype: str = "bf16"):
-        if dtype not in ("float32", "bf16"):
-            raise ValueError("AttentionDecode dtype must be 'float32' or 'bf16'")
+        if dtype not in _ATTN_DTYPES:
+            raise ValueError(f"AttentionDecode dtype must be one of {sorted(_ATTN_DTYPES)}, got {dtype!r}")
         self.scale = scale
         self.dtype = dtype
 
     def compute(self, q, k, v):
-        T = tb if self.dtype == "bf16" else tf
-        qt = T(np.asarray(q, np.float32), "gpu")
-        kt = T(np.asarray(k, np.float32), "gpu")
-        vt = T(np.asarray(v, np.float32), "gpu")
+        T = _ATTN_DTYPES[self.dtype]
+        qd, kd, vd = (T(np.asarray(x, np.float32), "gpu") for x in (q, k, v))
         out = T([1], "gpu")
-        d = qt.get_shape()[-1]
-        scale = float(np.float32(1.0 / math.sqrt(d))) if self.scale is None else float(self.scale)
-        ml.AttentionDecode(qt, kt, vt, out, scale)
+        scale = _default_scale(qd.get_shape()[-1]) if self.scale is None else float(self.scale)
+        ml.AttentionDecode(qd, kd, vd, out, scale)
         return out.numpy()
 
     def gradient(self, out_grad, node):
@@ -545,27 +515,24 @@ def attention_decode(q, k, v, scale: Optional[float] = None, dtype: str = "bf16"
     return AttentionDecode(scale, dtype)(q, k, v)
 
 
-# --------------------------------------------------------------- reference composition
+# ------------------------------------------------------------------ the composition the fused op replaces
 
 def causal_mask(Lq: int, Lk: int, dtype=np.float32) -> np.ndarray:
-    """The constant additive mask: -inf strictly above the diagonal."""
-    m = np.zeros((Lq, Lk), dtype=dtype)
-    m[np.triu_indices(Lq, 1, Lk)] = -np.inf
-    return m
+    """The constant additive mask: -inf where key > query, 0 elsewhere."""
+    return np.where(np.arange(Lk)[None, :] > np.arange(Lq)[:, None], -np.inf, 0.0).astype(dtype)
 
 
 def attention_composed(q: Tensor, k: Tensor, v: Tensor, causal: bool = False, scale: Optional[float] = None):
-    """Attention written with the reference's own autodiff ops, in its op
-    order: MatMul(Q, Transpose(K)) -> MulScalar -> EWiseAdd(mask) -> shift by
-    the (constant) row max -> Exp -> Summation -> Reshape -> BroadcastTo ->
-    EWiseDiv -> MatMul(., V).  Runs on the CPU through numpy; used to check
-    the fused op against the composition it replaces."""
-    d = q.shape[-1]
-    s = float(np.float32(1.0 / math.sqrt(d))) if scale is None else float(scale)
+    """Attention built from this module's numpy operators in the reference's
+    op order: MatMul(Q, Transpose(K)) -> MulScalar -> EWiseAdd(mask) -> shift
+    by the (constant) row max -> Exp -> Summation -> Reshape -> BroadcastTo ->
+    EWiseDiv -> MatMul(., V).  Runs on the host; used to check the fused
+    operator against the composition it replaces."""
+    s = _default_scale(q.shape[-1]) if scale is None else float(scale)
     scores = (q @ k.transpose()) * s
     if causal:
         scores = scores + Tensor(causal_mask(q.shape[-2], k.shape[-2], scores.dtype), requires_grad=False)
-    shift = Tensor(np.max(scores.numpy(), axis=-1, keepdims=True), requires_grad=False)
+    shift = _const(np.max(scores.numpy(), axis=-1, keepdims=True))
     e = exp(scores - broadcast_to(shift, scores.shape))
     z = summation(e, axes=(len(e.shape) - 1,))
     zb = broadcast_to(reshape(z, tuple(z.shape) + (1,)), e.shape)

@@ -33,6 +33,9 @@ _SIGS = {
     "tt_device_count": (C.c_int, [C.POINTER(C.c_int)]),
     "tt_init": (C.c_int, [C.c_int]),
     "tt_stream": (_p, []),
+    "tt_stream_create": (C.c_int, [C.POINTER(_p)]),
+    "tt_stream_sync": (C.c_int, [_p]),
+    "tt_stream_destroy": (C.c_int, [_p]),
     "tt_malloc": (C.c_int, [C.POINTER(_p), C.c_size_t]),
     "tt_free": (C.c_int, [_p]),
     "tt_empty_cache": (C.c_int, []),
@@ -256,6 +259,31 @@ def softmax_rows(x: DeviceBuffer, y: DeviceBuffer, stream=None):
     cols = x.shape[-1] if len(x.shape) else 1
     rows = (int(np.prod(x.shape[:-1])) if len(x.shape) > 1 else 1) if cols else 0
     lib().call("tt_softmax_rows_f32", x.ptr, y.ptr, rows, cols, stream)
+
+
+class Stream:
+    """A caller stream (tt_stream_create; default priority).  ``handle`` is
+    what the launchers take as their stream argument."""
+
+    def __init__(self):
+        self.L = lib()
+        s = C.c_void_p()
+        self.L.call("tt_stream_create", C.byref(s))
+        self.handle = s.value
+
+    def sync(self):
+        self.L.call("tt_stream_sync", self.handle)
+
+    def destroy(self):
+        if self.handle:
+            self.L.call("tt_stream_destroy", self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.destroy()
+        except Exception:
+            pass
 
 
 class Event:

@@ -10,6 +10,7 @@ Full-size configs are checked on sampled heads against the oracle and, over
 every head, through size-independent identities of the exact result:
   sum_j dV_j = sum_i dO_i      (rows of P sum to 1)
   sum_j dK_j = 0               (rows of dS sum to 0)
+  sum_i dQ_i . Q_i = sum_j dK_j . K_j   (both s sum_ij dS_ij q_i . k_j)
   causal: O[0] = V[0] and LSE[0] = s q_0 . k_0
 """
 import math
@@ -111,6 +112,15 @@ def _identities(name, x, o, lse, dq, dk, dv, scale, causal, tol):
     ref_scale = np.abs(dk.astype(np.float64)).sum(axis=2).max()
     _say(f"  {name} |sum_j dK_j| / sum_j |dK_j| = {sum_dk / ref_scale:.3e}")
     assert sum_dk <= tol * ref_scale
+    # sum_i dQ_i . Q_i = sum_j dK_j . K_j (both are s sum_ij dS_ij q_i . k_j), per
+    # head: ties dQ of every head to dK of the same head, so a dQ written to
+    # the wrong head or computed from another head's rows fails
+    lhs = np.einsum("bhld,bhld->bh", dq.astype(np.float64), x["q"].astype(np.float64))
+    rhs = np.einsum("bhld,bhld->bh", dk.astype(np.float64), x["k"].astype(np.float64))
+    norm = np.einsum("bhld,bhld->bh", np.abs(dq.astype(np.float64)), np.abs(x["q"].astype(np.float64))).max()
+    err = np.abs(lhs - rhs).max() / norm
+    _say(f"  {name} |sum dQ.Q - sum dK.K| / sum |dQ.Q| = {err:.3e}")
+    assert err <= tol
     if causal:
         _check(f"{name} O[0] = V[0]", o[:, :, 0], x["v"][:, :, 0], tol)
         s00 = scale * np.einsum("bhd,bhd->bh", x["q"][:, :, 0].astype(np.float64), x["k"][:, :, 0].astype(np.float64))

@@ -471,3 +471,22 @@ def test_planted_gemm_mistakes_are_caught():
     good = _brute_gemm(True, False, 1.0, A, B, 0.0, None)
     assert orc.max_rel_err(orc.gemm_f64(False, False, 1.0, A, B, 0.0), good) > 1e-3
     assert orc.max_rel_err(orc.gemm_f64(True, False, 1.0, B, A, 0.0), good) > 1e-3
+
+
+def test_dq_dk_contraction_identity_and_its_power():
+    """sum_i dQ_i . Q_i = sum_j dK_j . K_j per head (both are
+    s sum_ij dS_ij q_i . k_j): holds for the oracle, causal or not, and fails
+    when dQ of one head is swapped with another's (the mistake the GPU tests
+    use this identity to catch on heads the oracle does not sample)."""
+    rng = np.random.default_rng(31)
+    for causal in (False, True):
+        q, k, v, do = (rng.standard_normal((2, 3, 40, 32)) for _ in range(4))
+        dq, dk, _ = orc.attn_bwd_f64(q, k, v, do, 0.2, causal)
+        lhs = np.einsum("bhld,bhld->bh", dq, q)
+        rhs = np.einsum("bhld,bhld->bh", dk, k)
+        norm = np.einsum("bhld,bhld->bh", np.abs(dq), np.abs(q)).max()
+        assert np.abs(lhs - rhs).max() / norm < 1e-12
+        bad = dq.copy()
+        bad[0, 1], bad[1, 2] = dq[1, 2], dq[0, 1]
+        lhs_bad = np.einsum("bhld,bhld->bh", bad, q)
+        assert np.abs(lhs_bad - rhs).max() / norm > 2e-2
