@@ -190,6 +190,23 @@ int tt_attn_bwd_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                      int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t d,
                      float scale, int causal, void* stream);
 
+/* Allocation-free variant of tt_attn_bwd_bf16 (same arguments, kernels and
+ * results).  It has no counterpart in the reference; it is for callers that
+ * cannot allocate device memory: code under HIP graph capture, tight serving
+ * or training loops, harnesses that forbid hipMalloc.  Its row scratch (-D
+ * and LSE*log2(e), 8 bytes per query row) is a 16 MiB static device array per
+ * GPU, so B*H*Lq must not exceed 2097152 rows (TT_ERR_ARG beyond).  It calls
+ * no allocator and does no set-up: tt_init must have run (TT_ERR_ARG
+ * otherwise).  Every call on one GPU shares that array: calls that overlap
+ * on one GPU (two streams, or two host threads) race; order them.  The
+ * array keeps the last call's contents; each call writes every row it reads
+ * before reading it. */
+int tt_attn_bwd_bf16_noalloc(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                             const uint16_t* o, const float* lse, const uint16_t* do_,
+                             uint16_t* dq, uint16_t* dk, uint16_t* dv,
+                             int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t d,
+                             float scale, int causal, void* stream);
+
 /* Single-query decode: o = softmax(scale * q K^T) V per (b, h), no mask.
  * q [B,H,1,d], k/v cache [B,H,Lkv,d] contiguous, o [B,H,1,d], lse [B,H] (may
  * be NULL).  The same composition as the forward with Lq = 1 (a3 -> a4 -> a6

@@ -705,15 +705,13 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_pipe_kernel(
 }
 
 // ------------------------------------------------------------------ launchers
+// `delta`: device scratch of 2 * BH * Lq floats that the kernels of this call
+// own until they finish: -D (negated row sums of dO o O), then LSE * log2(e).
 template <typename T, int D, bool CAUSAL>
 static int launch_bwd(const T* q, const T* k, const T* v, const T* o, const float* lse, const T* dout,
-                      T* dq, T* dk, T* dv, int64_t BH, int64_t Lq, int64_t Lk, float scale, hipStream_t st) {
+                      T* dq, T* dk, T* dv, int64_t BH, int64_t Lq, int64_t Lk, float scale, hipStream_t st,
+                      float* delta) {
   constexpr bool BF = sizeof(T) == 2;
-  // workspace: -D (negated row sums of dO o O) and LSE * log2(e), fp32 [B*H*Lq] each
-  float* delta = nullptr;
-  WorkspaceLease ws;  // held until the kernels that read the buffer are launched
-  int rc = ws.get(st, kWsBackwardRows, (size_t)(2 * BH * Lq) * sizeof(float), (void**)&delta);
-  if (rc) return rc;
   const int64_t rows = BH * Lq;
   float* l2 = delta + rows;
   constexpr int TPR = D / (16 / (int)sizeof(T));
@@ -760,9 +758,29 @@ static int launch_bwd(const T* q, const T* k, const T* v, const T* o, const floa
 }
 
 template <typename T>
-static int bwd_entry(const char* fn, const T* q, const T* k, const T* v, const T* o, const float* lse,
-                     const T* dout, T* dq, T* dk, T* dv, int64_t B, int64_t H, int64_t Lq, int64_t Lk,
-                     int64_t d, float scale, int causal, void* stream) {
+static int dispatch_bwd(const char* fn, const T* q, const T* k, const T* v, const T* o, const float* lse,
+                        const T* dout, T* dq, T* dk, T* dv, int64_t BH, int64_t Lq, int64_t Lk, int64_t d, float scale,
+                        int causal, hipStream_t st, float* delta) {
+  switch (d * 2 + (causal ? 1 : 0)) {
+    case 64: return launch_bwd<T, 32, false>(q, k, v, o, lse, dout, dq, dk, dv, BH, Lq, Lk, scale, st, delta);
+    case 65: return launch_bwd<T, 32, true>(q, k, v, o, lse, dout, dq, dk, dv, BH, Lq, Lk, scale, st, delta);
+    case 128: return launch_bwd<T, 64, false>(q, k, v, o, lse, dout, dq, dk, dv, BH, Lq, Lk, scale, st, delta);
+    case 129: return launch_bwd<T, 64, true>(q, k, v, o, lse, dout, dq, dk, dv, BH, Lq, Lk, scale, st, delta);
+    case 256: return launch_bwd<T, 128, false>(q, k, v, o, lse, dout, dq, dk, dv, BH, Lq, Lk, scale, st, delta);
+    case 257: return launch_bwd<T, 128, true>(q, k, v, o, lse, dout, dq, dk, dv, BH, Lq, Lk, scale, st, delta);
+    default: return fail(TT_ERR_UNSUPPORTED, std::string(fn) + ": unsupported head dim");
+  }
+}
+
+// Shared argument checks of the backward entry points.  Returns TT_OK with
+// *done = true when nothing is left to launch (no heads, or no queries: then
+// dK and dV are zero-filled by a kernel, not a memset, so that the call can
+// sit inside a captured graph).
+template <typename T>
+static int bwd_prologue(const char* fn, const T* q, const T* k, const T* v, const T* o, const float* lse,
+                        const T* dout, T* dq, T* dk, T* dv, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t d,
+                        int causal, hipStream_t st, bool* done) {
+  *done = true;
   int rc = check_attn_shape(fn, B, H, Lq, Lk, d, causal);
   if (rc) return rc;
   const int64_t BH = B * H;
@@ -770,26 +788,37 @@ static int bwd_entry(const char* fn, const T* q, const T* k, const T* v, const T
   if (Lq == 0) {  // no queries: every key gets zero gradient
     if (Lk > 0) {
       if (!dk || !dv) return fail(TT_ERR_ARG, std::string(fn) + ": null pointer");
-      if ((rc = ensure_init())) return rc;
-      hipStream_t st = stream_or_default(stream);
-      TT_HIP(hipMemsetAsync(dk, 0, (size_t)(BH * Lk * d) * sizeof(T), st));
-      TT_HIP(hipMemsetAsync(dv, 0, (size_t)(BH * Lk * d) * sizeof(T), st));
+      const int dt = sizeof(T) == 2 ? TT_BF16 : TT_F32;
+      if ((rc = tt_elementwise(TT_EW_FILL, dt, dk, nullptr, nullptr, BH * Lk * d, 0.0, 0.0, 0, st))) return rc;
+      if ((rc = tt_elementwise(TT_EW_FILL, dt, dv, nullptr, nullptr, BH * Lk * d, 0.0, 0.0, 0, st))) return rc;
     }
     return ok();
   }
   if (!q || !k || !v || !o || !lse || !dout || !dq || !dk || !dv)
     return fail(TT_ERR_ARG, std::string(fn) + ": null pointer");
+  *done = false;
+  return TT_OK;
+}
+
+template <typename T>
+static int bwd_entry(const char* fn, const T* q, const T* k, const T* v, const T* o, const float* lse,
+                     const T* dout, T* dq, T* dk, T* dv, int64_t B, int64_t H, int64_t Lq, int64_t Lk,
+                     int64_t d, float scale, int causal, void* stream) {
+  int rc = check_attn_shape(fn, B, H, Lq, Lk, d, causal);
+  if (rc) return rc;
+  if (B * H == 0) return ok();
+  if (Lq > 0 && (!q || !k || !v || !o || !lse || !dout || !dq || !dk || !dv))  // before touching the device
+    return fail(TT_ERR_ARG, std::string(fn) + ": null pointer");
   if ((rc = ensure_init())) return rc;
   hipStream_t st = stream_or_default(stream);
-  switch (d * 2 + (causal ? 1 : 0)) {
-    case 64: return launch_bwd<T, 32, false>(q, k, v, o, lse, dout, dq, dk, dv, BH, Lq, Lk, scale, st);
-    case 65: return launch_bwd<T, 32, true>(q, k, v, o, lse, dout, dq, dk, dv, BH, Lq, Lk, scale, st);
-    case 128: return launch_bwd<T, 64, false>(q, k, v, o, lse, dout, dq, dk, dv, BH, Lq, Lk, scale, st);
-    case 129: return launch_bwd<T, 64, true>(q, k, v, o, lse, dout, dq, dk, dv, BH, Lq, Lk, scale, st);
-    case 256: return launch_bwd<T, 128, false>(q, k, v, o, lse, dout, dq, dk, dv, BH, Lq, Lk, scale, st);
-    case 257: return launch_bwd<T, 128, true>(q, k, v, o, lse, dout, dq, dk, dv, BH, Lq, Lk, scale, st);
-    default: return fail(TT_ERR_UNSUPPORTED, std::string(fn) + ": unsupported head dim");
-  }
+  bool done = false;
+  if ((rc = bwd_prologue(fn, q, k, v, o, lse, dout, dq, dk, dv, B, H, Lq, Lk, d, causal, st, &done)) || done)
+    return rc;
+  const int64_t BH = B * H;
+  float* delta = nullptr;
+  WorkspaceLease ws;  // held until the kernels that read the buffer are launched
+  if ((rc = ws.get(st, kWsBackwardRows, (size_t)(2 * BH * Lq) * sizeof(float), (void**)&delta))) return rc;
+  return dispatch_bwd(fn, q, k, v, o, lse, dout, dq, dk, dv, BH, Lq, Lk, d, scale, causal, st, delta);
 }
 
 }  // namespace tt
@@ -810,4 +839,29 @@ extern "C" int tt_attn_bwd_bf16(const uint16_t* q, const uint16_t* k, const uint
                                 int64_t d, float scale, int causal, void* stream) {
   return bwd_entry<u16>("tt_attn_bwd_bf16", q, k, v, o, lse, do_, dq, dk, dv, B, H, Lq, Lk, d, scale,
                         causal, stream);
+}
+
+// The bf16 backward with its row scratch in the library's static device
+// array instead of an allocated workspace (see include/tt_attn.h).
+extern "C" int tt_attn_bwd_bf16_noalloc(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                        const uint16_t* o, const float* lse, const uint16_t* do_, uint16_t* dq,
+                                        uint16_t* dk, uint16_t* dv, int64_t B, int64_t H, int64_t Lq, int64_t Lk,
+                                        int64_t d, float scale, int causal, void* stream) {
+  const char* fn = "tt_attn_bwd_bf16_noalloc";
+  int rc = check_attn_shape(fn, B, H, Lq, Lk, d, causal);
+  if (rc) return rc;
+  if (B * H == 0) return ok();
+  size_t cap = 0;
+  float* scratch = static_cast<float*>(noalloc_scratch(&cap));
+  if (!scratch)
+    return fail(TT_ERR_ARG, std::string(fn) + ": call tt_init first (this entry point does no set-up of its own)");
+  if (B * H * Lq > (int64_t)(cap / (2 * sizeof(float))))
+    return fail(TT_ERR_ARG, std::string(fn) + ": B*H*Lq = " + std::to_string(B * H * Lq) +
+                                " rows exceed the static scratch maximum of " +
+                                std::to_string(cap / (2 * sizeof(float))) + " rows");
+  hipStream_t st = stream_or_default(stream);
+  bool done = false;
+  if ((rc = bwd_prologue<u16>(fn, q, k, v, o, lse, do_, dq, dk, dv, B, H, Lq, Lk, d, causal, st, &done)) || done)
+    return rc;
+  return dispatch_bwd<u16>(fn, q, k, v, o, lse, do_, dq, dk, dv, B * H, Lq, Lk, d, scale, causal, st, scratch);
 }

@@ -26,6 +26,12 @@ int ensure_init();
 // kernel launch on `s`; a no-op unless instrumentation is enabled.
 void after_launch(hipStream_t s);
 
+// The allocation-free backward's scratch: a static device array of
+// kNoAllocScratchBytes whose device address tt_init looks up once per
+// device.  Returns nullptr before tt_init; *bytes gets the array's size.
+constexpr size_t kNoAllocScratchBytes = size_t(16) << 20;
+void* noalloc_scratch(size_t* bytes);
+
 // Device scratch of the attention launchers: one buffer per (stream, user),
 // grown on demand and kept for reuse.  A lease holds the workspace lock from
 // get() until it is destroyed: keep it alive until every kernel that reads

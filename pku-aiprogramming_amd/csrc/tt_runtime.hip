@@ -89,6 +89,21 @@ void after_launch(hipStream_t s) {
   (void)hipEventRecord((hipEvent_t)g_launch_events[g_launch_next++], s);
 }
 
+// ---------------------------------------------------------------- allocation-free scratch
+// Row scratch of tt_attn_bwd_bf16_noalloc (-D and LSE * log2(e) of up to
+// 2 Mi query rows).  Every GPU holds its own copy until the process ends;
+// host code uses the device address tt_init looked up, never the array's
+// name (which on the host is only a stand-in for the symbol).
+static __device__ __align__(256) float scratch[kNoAllocScratchBytes / sizeof(float)];
+constexpr int kMaxDevices = 64;
+static void* g_scratch_ptr[kMaxDevices] = {};
+
+void* noalloc_scratch(size_t* bytes) {
+  if (bytes) *bytes = kNoAllocScratchBytes;
+  if (!g_inited) return nullptr;
+  return g_scratch_ptr[g_device];
+}
+
 // ---------------------------------------------------------------- workspace
 struct WorkspaceLease::Impl {
   WorkspaceCache<HipBackend>::Lease lease{g_ws};
@@ -241,7 +256,12 @@ int tt_init(int device) {
     return fail(TT_ERR_HIP, "tt_init: no HIP device available");
   }
   if (device < 0 || device >= n) return fail(TT_ERR_ARG, "tt_init: device index out of range");
+  if (device >= kMaxDevices) return fail(TT_ERR_ARG, "tt_init: device index above the supported 64");
   TT_HIP(hipSetDevice(device));
+  // once per device, with that device current: its copy of the static scratch
+  void* sp = nullptr;
+  TT_HIP(hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch)));
+  g_scratch_ptr[device] = sp;
   // Default priority on purpose: one stream, ordinary priority.
   TT_HIP(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
   g_device = device;

@@ -60,6 +60,7 @@ _SIGS = {
     "tt_attn_fwd_bf16": (C.c_int, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, C.c_float, C.c_int, _p]),
     "tt_attn_bwd_f32": (C.c_int, [_p] * 9 + [_i64] * 5 + [C.c_float, C.c_int, _p]),
     "tt_attn_bwd_bf16": (C.c_int, [_p] * 9 + [_i64] * 5 + [C.c_float, C.c_int, _p]),
+    "tt_attn_bwd_bf16_noalloc": (C.c_int, [_p] * 9 + [_i64] * 5 + [C.c_float, C.c_int, _p]),
     "tt_attn_decode_bf16": (C.c_int, [_p] * 5 + [_i64] * 4 + [C.c_float, _p]),
     "tt_attn_decode_f32": (C.c_int, [_p] * 5 + [_i64] * 4 + [C.c_float, _p]),
     "tt_softmax_rows_f32": (C.c_int, [_p, _p, _i64, _i64, _p]),
