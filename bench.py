@@ -148,6 +148,110 @@ def run_decode(T, steps, warmup):
     return total_ms / steps, per
 
 
+# The other BASELINE.json configurations (parity configs c1-c3), each timed
+# as one step = forward (+ backward when the config has one) with HIP events
+# over `steps` steps, inputs resident in HBM.  fp32 configs are priced
+# against the fp32 MFMA peak, bf16 against the bf16 one.
+PEAK_FP32_MFMA_TFLOPS = 157.3
+
+
+def config_flops(cfg):
+    f = (12.0 if cfg.backward else 4.0) * cfg.B * cfg.H * cfg.Lq * cfg.Lk * cfg.d
+    return f / 2 if cfg.causal else f
+
+
+def run_config(T, cfg, steps, warmup):
+    dt = cfg.dtype
+    qs, ks = (cfg.B, cfg.H, cfg.Lq, cfg.d), (cfg.B, cfg.H, cfg.Lk, cfg.d)
+    q, do_ = T.DeviceBuffer(qs, dt), T.DeviceBuffer(qs, dt)
+    k, v = T.DeviceBuffer(ks, dt), T.DeviceBuffer(ks, dt)
+    for i, b in enumerate((q, k, v, do_)):
+        b.fill_normal(6100 + 10 * cfg.cid + i, cfg.qkv_scale if i < 3 else 1.0)
+    o = T.DeviceBuffer(qs, dt)
+    lse = T.DeviceBuffer(qs[:3], "f32")
+    g = [T.DeviceBuffer(qs, dt), T.DeviceBuffer(ks, dt), T.DeviceBuffer(ks, dt)]
+
+    def step():
+        T.attn_fwd(q, k, v, o, lse, cfg.scale, cfg.causal)
+        if cfg.backward:
+            T.attn_bwd(q, k, v, o, lse, do_, *g, cfg.scale, cfg.causal)
+
+    for _ in range(warmup):
+        step()
+    T.lib().sync()
+    a, b = T.Event(), T.Event()
+    a.record()
+    for _ in range(steps):
+        step()
+    b.record()
+    T.lib().sync()
+    return T.Event.elapsed(a, b) / steps
+
+
+def config_cpu_baseline(cfg, max_heads, reps=3):
+    """The reference's op chain (oracle composition_*_f32, float32 numpy, full
+    L x L materialised) on up to `max_heads` heads of the config; returns the
+    rate in TFLOP/s of the same algorithmic FLOP count."""
+    import numpy as np
+
+    from oracle import attn_oracle as orc
+
+    x = orc.seeded_inputs(cfg)
+    heads = [(b, h) for b in range(cfg.B) for h in range(cfg.H)][:max_heads]
+
+    def once():
+        for b, h in heads:
+            if cfg.backward:
+                orc.composition_bwd_f32(x["q"][b, h], x["k"][b, h], x["v"][b, h], x["do"][b, h], cfg.scale, cfg.causal)
+            else:
+                orc.composition_fwd_f32(x["q"][b, h], x["k"][b, h], x["v"][b, h], cfg.scale, cfg.causal)
+
+    once()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        once()
+        ts.append(time.perf_counter() - t0)
+    t = sorted(ts)[len(ts) // 2]
+    frac = len(heads) / (cfg.B * cfg.H)
+    return {"value": config_flops(cfg) * frac / t / 1e12, "unit": "TFLOP/s", "cores": int(_blas_threads()),
+            "kind": "port", "seconds": t,
+            "sample": f"{len(heads)} of {cfg.B * cfg.H} heads, reference op order in float32 numpy "
+                      f"(median of {reps}: {t * 1e3:.1f} ms)"}
+
+
+def decode_cpu_baseline(heads=256, reps=3):
+    """The reference's op chain for one query (Q @ K^T, * s, softmax, @ V) in
+    float32 numpy over `heads` (b, h) heads of the decode workload: K/V bytes
+    read per second (bf16-sized, as on the GPU)."""
+    import numpy as np
+
+    B, H, Lkv, d = C4["B"], C4["H"], C4["Lkv"], C4["d"]
+    rng = np.random.default_rng(4)
+    k = rng.standard_normal((heads, Lkv, d), dtype=np.float32)
+    v = rng.standard_normal((heads, Lkv, d), dtype=np.float32)
+    q = rng.standard_normal((heads, 1, d), dtype=np.float32)
+    s = np.float32(1.0 / math.sqrt(d))
+
+    def once():
+        sc = np.matmul(q, np.swapaxes(k, -1, -2)) * s
+        sc = sc - sc.max(axis=-1, keepdims=True)
+        e = np.exp(sc)
+        return np.matmul(e / e.sum(axis=-1, keepdims=True), v)
+
+    once()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        once()
+        ts.append(time.perf_counter() - t0)
+    t = sorted(ts)[len(ts) // 2]
+    nbytes = heads * (2 * Lkv * d * 2 + 2 * d * 2)
+    return {"value": nbytes / t / 1e9, "unit": "GB/s", "cores": int(_blas_threads()), "kind": "port",
+            "sample": f"{heads} of {B * H} heads (Lkv={Lkv}, d={d}), float32 numpy, bytes counted as bf16 "
+                      f"(median of {reps}: {t * 1e3:.1f} ms)"}
+
+
 def run_copy(T, steps, warmup, nbytes=1 << 30):
     """Plain fp32 copy (c = 1.0 * a) of `nbytes`: reads and writes exactly
     nbytes each, used to calibrate the profiler's FETCH_SIZE / WRITE_SIZE."""
@@ -206,7 +310,6 @@ GEMM_CASES = [
     dict(dtype="bf16", m=8192, n=8192, k=8192, ta=False, tb=False),
     dict(dtype="bf16", m=8192, n=8192, k=8192, ta=True, tb=True),
 ]
-PEAK_FP32_MFMA_TFLOPS = 157.3
 
 
 def run_gemm(T, steps, warmup, dtype, m, n, k, ta, tb):
@@ -414,7 +517,8 @@ def main(argv=None):
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", choices=["all", "fwdbwd", "decode", "copy", "ceiling", "softmax", "gemm", "io"], default="all",
+    ap.add_argument("--only", choices=["all", "fwdbwd", "configs", "decode", "copy", "ceiling", "softmax", "gemm", "io"],
+                    default="all",
                     help="run one workload only (for profiler runs; 'copy' is the 1 GiB calibration copy, "
                          "'ceiling' the library bf16 GEMM reference)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -491,11 +595,33 @@ def main(argv=None):
                          "unit": "GB/s", "frac": sgbs / PEAK_HBM_GBS, "traffic": traffic_bytes("attn_decode_split"),
                          "algorithmic_bytes_per_launch": split_bytes},
         }
+        if not args.no_cpu_baseline:
+            out["decode"]["cpu_baseline"] = decode_cpu_baseline()
         if args.only == "decode":
             out["metric"], out["dtype"] = "attn decode KV-read HBM GB/s", "bf16"
             out["config"] = {"workload": out["decode"]["workload"], **C4}
             out["value"], out["unit"], out["ms_per_step"] = gbs, "GB/s", ms
             out["roofline"] = out["decode"]["roofline"]
+
+    if args.only in ("all", "configs"):
+        sys.path.insert(0, ROOT)
+        from oracle import attn_oracle as orc
+
+        lines = []
+        for cid in (1, 2, 3):
+            cfg = orc.CONFIGS[cid]
+            ms = run_config(T, cfg, max(args.steps, 20), args.warmup)
+            tf = config_flops(cfg) / (ms * 1e-3) / 1e12
+            peak = PEAK_BF16_TFLOPS if cfg.dtype == "bf16" else PEAK_FP32_MFMA_TFLOPS
+            work = (f"{'causal ' if cfg.causal else ''}attention {'fwd+bwd' if cfg.backward else 'fwd'} {cfg.dtype}, "
+                    f"B={cfg.B} H={cfg.H} L={cfg.Lq} d={cfg.d}")
+            line = {"config": f"c{cid}", "workload": work, "dtype": cfg.dtype,
+                    "flop_per_step": config_flops(cfg), "ms_per_step": ms, "value": tf, "unit": "TFLOP/s",
+                    "peak": peak, "frac_of_peak": tf / peak}
+            if not args.no_cpu_baseline:
+                line["cpu_baseline"] = config_cpu_baseline(cfg, max_heads={1: 1, 2: 64, 3: 32}[cid])
+            lines.append(line)
+        out["configs"] = lines
 
     if args.only in ("all", "softmax"):
         cases = []

@@ -35,38 +35,22 @@
 
 namespace tt {
 
-// Waves per workgroup, pipeline depth, and tile sizes of the bf16 kernels.
-// Default: 4-wave workgroups with 2 stages, so two workgroups with
-// independent barriers share each CU (2 waves per SIMD); measured faster on
-// the MI355X than one 8-wave workgroup with a 4-deep ring.
-#ifndef TT_BWD_WAVES
-#define TT_BWD_WAVES 4
-#endif
-#ifndef TT_BWD_STAGES
-#define TT_BWD_STAGES 2
-#endif
-constexpr int bwd_nw(int D) { return D == 32 ? 4 : TT_BWD_WAVES; }
-constexpr int kBwdStages = TT_BWD_STAGES;
-static_assert(kBwdStages >= 2 && kBwdStages <= 4, "tile ring depth must be 2..4");
-constexpr int DQ_BN = 64;  // keys per LDS tile of the dQ kernel
-#ifndef TT_DQ_PIPE
-#define TT_DQ_PIPE 1
-#endif
-// Query rows per LDS tile of the dK/dV kernel: the ring of Q / dO tiles
-// plus the V rows of the workgroup fit 160 KB of LDS.
-#ifndef TT_DKDV_BQ128
-#define TT_DKDV_BQ128 32
-#endif
-constexpr int dkdv_bq(int D) { return D == 128 ? TT_DKDV_BQ128 : 64; }
+// Waves per workgroup, pipeline depth, and tile sizes of the bf16 kernels:
+// 4-wave workgroups with 2 stages, so two workgroups with independent
+// barriers share each CU (2 waves per SIMD); measured faster on the MI355X
+// than one 8-wave workgroup with a 4-deep ring.
+constexpr int bwd_nw(int) { return 4; }
+constexpr int kBwdStages = 2;
+constexpr int DQ_BN = 64;  // keys per LDS tile of the d = 32 dQ kernel
+// Query rows per LDS tile of the dK/dV kernel: the ring of Q / dO tiles plus
+// the V rows of the workgroup fit 160 KB of LDS.
+constexpr int dkdv_bq(int D) { return D == 128 ? 32 : 64; }
 // K chunks (16 columns each) the dK/dV kernel keeps in LDS rather than in
 // registers.  At d = 128 the dK / dV accumulators (128 VGPRs) and the K rows
 // (32) leave too little of the 256 registers of a 2-waves-per-SIMD kernel;
 // each parked chunk frees 4 VGPRs for one extra 16-byte LDS read per query
 // tile.
-#ifndef TT_DKDV_KLDS
-#define TT_DKDV_KLDS 3
-#endif
-constexpr int dkdv_klds(int D) { return D == 128 ? TT_DKDV_KLDS : 0; }
+constexpr int dkdv_klds(int D) { return D == 128 ? 3 : 0; }
 
 // ND_i = -D_i = -sum_d dO[i][d] * O[i][d], one 16-byte chunk per thread
 // (stored negated: the dK/dV kernel starts its dP accumulator at -D, so the
@@ -732,7 +716,7 @@ static int launch_bwd(const T* q, const T* k, const T* v, const T* o, const floa
     hipLaunchKernelGGL((attn_bwd_dkdv_bf16_kernel<D, CAUSAL>), dim3((unsigned)(nkt * BH)), dim3(64 * NW), 0, st, q,
                        k, v, dout, l2, delta, dk, dv, (int)Lq, (int)Lk, (int)BH, (int)nkt, gk, sl2, scale);
     TT_LAUNCHED("attention backward dK/dV launch", st);
-    if constexpr (D >= 64 && TT_DQ_PIPE) {
+    if constexpr (D >= 64) {
       const int64_t nqp = (Lq + 127) / 128;
       const int gp = pick_group(BH, nqp, 32 * 2);
       hipLaunchKernelGGL((attn_bwd_dq_pipe_kernel<D, CAUSAL>), dim3((unsigned)(nqp * BH)), dim3(256), 0, st, q, k, v,

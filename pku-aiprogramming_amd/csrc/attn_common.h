@@ -87,11 +87,6 @@ __device__ __forceinline__ float sum_bf16x2(const bf16x8& v, int e, float acc) {
   return __builtin_amdgcn_fdot2_f32_bf16(pair, one, acc, false);
 }
 
-// Instruction classes of __builtin_amdgcn_sched_group_barrier.
-constexpr int kSchedMFMA = 0x008;
-constexpr int kSchedVALU = 0x002 | 0x400;  // VALU incl. transcendental
-constexpr int kSchedDSRead = 0x100;
-
 // Exact power-of-two exponent: v_exp_f32 computes 2^x.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 

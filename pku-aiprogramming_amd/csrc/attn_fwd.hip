@@ -27,18 +27,11 @@
 namespace tt {
 
 constexpr int FWD_BN = 64;  // keys per LDS tile
-// Waves per workgroup and pipeline depth (K/V tiles in flight) of the bf16
-// kernel.  Default: 4-wave workgroups with 2 stages (64 KB of LDS at
-// d = 128), so two workgroups with independent barriers share each CU.
-#ifndef TT_FWD_WAVES
-#define TT_FWD_WAVES 4
-#endif
-#ifndef TT_FWD_STAGES
-#define TT_FWD_STAGES 2
-#endif
-constexpr int fwd_nw(int D) { return D == 32 ? 4 : TT_FWD_WAVES; }
-constexpr int kStages = TT_FWD_STAGES;
-static_assert(kStages >= 2 && kStages <= 4, "K/V ring depth must be 2..4");
+// Waves per workgroup and pipeline depth (K/V tiles in flight) of the simple
+// bf16 kernel (d = 32): 4-wave workgroups with 2 stages, so two workgroups
+// with independent barriers share each CU.
+constexpr int fwd_nw(int) { return 4; }
+constexpr int kStages = 2;
 constexpr int FWD_F32_BM = 128;  // queries per workgroup of the fp32 kernel
 
 template <int D, bool CAUSAL>
@@ -246,22 +239,10 @@ __global__ __launch_bounds__(64 * fwd_nw(D), 8 / fwd_nw(D)) void attn_fwd_bf16_k
 // V_n) is waited for at barrier n (before iteration n) and pair n + 1 is
 // issued right after it into the buffers of K_n and V_{n-1}, which
 // iterations up to n - 1 have finished with.
-#ifndef TT_FWDP_NW
-#define TT_FWDP_NW 4
-#endif
-constexpr int FWDP_NW = TT_FWDP_NW;  // waves per workgroup
-// Interleave MFMA / VALU / LDS reads by sched_group_barrier (1) or leave the
-// order to the compiler's scheduler (0): the compiler's is 3 % faster on the
-// MI355X with the current loop body.
-#ifndef TT_FWDP_SCHED
-#define TT_FWDP_SCHED 0
-#endif
-#ifndef TT_FWDP_KAHEAD
-#define TT_FWDP_KAHEAD 2  // K chunks read ahead of their MFMAs
-#endif
-#ifndef TT_FWDP_VAHEAD
-#define TT_FWDP_VAHEAD 3  // V^T operands read ahead of their MFMAs
-#endif
+// 4-wave workgroups, two per CU (8-wave workgroups measured 6 % slower).
+// The compiler's scheduler interleaves the VALU and MFMA work of the loop
+// body (an explicit sched_group_barrier pattern measured 3 % slower).
+constexpr int FWDP_NW = 4;
 
 template <int D, bool CAUSAL, int NW>
 __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fwd_bf16_pipe_kernel(
@@ -428,43 +409,6 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fwd_bf16_pipe_kernel(
     issue_v(n + 1);
   };
 
-  // Interleave patterns: one MFMA at a time with the VALU work that fits
-  // beside it; LDS operand reads run TT_FWDP_KAHEAD K chunks / TT_FWDP_VAHEAD
-  // V^T operands ahead of the MFMAs that consume them, and the first V^T
-  // operands are fetched at the end of phase 1.
-  constexpr int kP1Mfma = 2 * NC, kP1Valu = 32 * 2 + 16 + 2;
-  constexpr int kP1VPer = (kP1Valu + kP1Mfma - 1) / kP1Mfma;
-  constexpr int kP2Mfma = 4 * ND, kP2Valu = 16 + 20 + 12;
-  constexpr int kP2VPer = (kP2Valu + kP2Mfma - 1) / kP2Mfma;
-  constexpr int KA = TT_FWDP_KAHEAD < NC ? TT_FWDP_KAHEAD : NC;
-  constexpr int VA = TT_FWDP_VAHEAD < 4 * ND ? TT_FWDP_VAHEAD : 4 * ND;
-  auto sched_phase1 = [&]() {
-    if constexpr (TT_FWDP_SCHED) {
-      __builtin_amdgcn_sched_group_barrier(kSchedDSRead, 2 * KA, 0);
-      __builtin_amdgcn_sched_group_barrier(kSchedVALU, 4, 0);
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        if (c + KA < NC) __builtin_amdgcn_sched_group_barrier(kSchedDSRead, 2, 0);
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-          __builtin_amdgcn_sched_group_barrier(kSchedMFMA, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(kSchedVALU, kP1VPer, 0);
-        }
-      }
-      __builtin_amdgcn_sched_group_barrier(kSchedDSRead, 2 * VA, 0);
-    }
-  };
-  auto sched_phase2 = [&]() {
-    if constexpr (TT_FWDP_SCHED) {
-#pragma unroll
-      for (int i = 0; i < 4 * ND; ++i) {
-        if (i + VA < 4 * ND) __builtin_amdgcn_sched_group_barrier(kSchedDSRead, 2, 0);
-        __builtin_amdgcn_sched_group_barrier(kSchedMFMA, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(kSchedVALU, kP2VPer, 0);
-      }
-    }
-  };
-
   // Iteration j: barrier j, S_{j+1} from K_{j+1} into `nx` while the
   // softmax of `cur` (tile j) runs, then PV of tile j and the max of tile j + 1.
   // PAR = j & 1 when known at compile time (the buffers' LDS offsets then
@@ -498,12 +442,10 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fwd_bf16_pipe_kernel(
     else
       qk(sK + kbuf * TE, nx, no_load);
     exp_cvt(cur);
-    sched_phase1();
     pv(sV + vbuf * TE);
     add_sum();
     if constexpr (MASK) mask_tile(nx, BN * (j + 1));
     rescale = row_max(nx, false);
-    sched_phase2();
   };
 
   // Prologue: K_0, then pair 0 (K_1, V_0); S_0 once K_0 has landed.

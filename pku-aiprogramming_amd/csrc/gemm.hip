@@ -39,13 +39,6 @@ namespace {
 
 constexpr int GM = 128;  // C tile rows per workgroup
 
-#ifndef TT_GEMM_WIDE
-#define TT_GEMM_WIDE 1
-#endif
-#ifndef TT_GEMM_SWZ
-#define TT_GEMM_SWZ 1
-#endif
-
 template <typename T>
 struct GemmT;
 template <>
@@ -62,9 +55,8 @@ template <>
 struct GemmT<u16> {
   // 128 x 256 tiles (each wave 64 x 128) halve the operand traffic per MFMA
   // of 128 x 128 ones; BK = 32 keeps two workgroups' rings in LDS
-  static constexpr int GN = TT_GEMM_WIDE ? 256 : 128;
-  static constexpr int BK = TT_GEMM_WIDE ? 32 : 64, EPC = 8;
-#if TT_GEMM_SWZ
+  static constexpr int GN = 256;
+  static constexpr int BK = 32, EPC = 8;
   // LDS has 64 banks of 4 bytes.  k-contiguous tiles: unpadded rows whose
   // 16-byte chunks are XOR-swizzled by row, so that both the 16 rows of a
   // 16-lane ds_read_b128 and the 4 rows x 4 chunks of a 16-lane store hit 16
@@ -74,11 +66,6 @@ struct GemmT<u16> {
   static constexpr int PAD_K = 0;
   static constexpr int PAD_R = 32;
   static constexpr bool SWZ = true;
-#else
-  static constexpr int PAD_K = 8;
-  static constexpr int PAD_R = 16;
-  static constexpr bool SWZ = false;
-#endif
   static __device__ __forceinline__ float to_f(u16 x) { return bf16_to_f32(x); }
   static __device__ __forceinline__ u16 from_f(float x) { return f32_to_bf16(x); }
 };
@@ -259,19 +246,13 @@ __global__ __launch_bounds__(256, 2) void k_gemm(int M, int N, int K, float alph
     }
 }
 
-// The direct-to-LDS kernel below serves full bf16 tiles (1); 0 sends every
-// call to k_gemm.  A 2-deep ring (48 KB of LDS, 155-167 VGPRs: three
-// workgroups per CU) measured 1075-1093 TF at 8192^3 against 985-1018 for 3
-// stages and 845-892 for 4 (one or two workgroups per CU).
-#ifndef TT_GEMM_DMA
-#define TT_GEMM_DMA 1
-#endif
-#ifndef TT_GEMM_DMA_S
-#define TT_GEMM_DMA_S 2
-#endif
-#ifndef TT_GEMM_DMA_GN
-#define TT_GEMM_DMA_GN 256  // C tile columns per workgroup (128: 91 VGPRs but 15-20 % slower)
-#endif
+// The direct-to-LDS kernel below serves full bf16 tiles.  A 2-deep ring (48
+// KB of LDS, 155-167 VGPRs: three workgroups per CU) measured 1075-1093 TF at
+// 8192^3 against 985-1018 for 3 stages and 845-892 for 4 (one or two
+// workgroups per CU); 256 C columns per workgroup (128: 91 VGPRs but 15-20 %
+// slower).
+constexpr int kDmaStages = 2;
+constexpr int kDmaGN = 256;
 
 // bf16 kernel for k % 32 == 0 with 16-byte aligned operands (ragged m and n
 // allowed): tiles go straight from global memory into LDS
@@ -333,7 +314,7 @@ __global__ __launch_bounds__(256, 3) void k_gemm_dma(int M, int N, int K, float 
                                                     int64_t lda, const u16* __restrict__ B, int64_t ldb,
                                                     float beta, u16* C) {
   using G = GemmT<u16>;
-  constexpr int GN = TT_GEMM_DMA_GN, NB = GN / 64, BK = 32, KS = BK / 16, S = TT_GEMM_DMA_S;
+  constexpr int GN = kDmaGN, NB = GN / 64, BK = 32, KS = BK / 16, S = kDmaStages;
   using TileA = DmaTile<GM, !TA>;
   using TileB = DmaTile<GN, TB>;
   constexpr int PER = TileA::LOADS + TileB::LOADS;
@@ -421,8 +402,8 @@ int gemm_launch(const char* fn, int transa, int transb, int64_t m, int64_t n, in
   if constexpr (sizeof(T) == 2) {
     // k in whole steps, aligned rows (m, n multiples of 8 where they are the
     // contiguous axis: vec), and every per-lane tile offset within 32 bits
-    if (TT_GEMM_DMA && vec && k % 32 == 0 && lda < (int64_t(1) << 22) && ldb < (int64_t(1) << 22)) {
-      const dim3 g2((unsigned)((n + TT_GEMM_DMA_GN - 1) / TT_GEMM_DMA_GN), (unsigned)gy);
+    if (vec && k % 32 == 0 && lda < (int64_t(1) << 22) && ldb < (int64_t(1) << 22)) {
+      const dim3 g2((unsigned)((n + kDmaGN - 1) / kDmaGN), (unsigned)gy);
 #define TT_GEMM_D(TA, TB) \
   hipLaunchKernelGGL((k_gemm_dma<TA, TB>), g2, dim3(256), 0, s, (int)m, (int)n, (int)k, alpha, A, lda, B, ldb, beta, C)
       switch (transa * 2 + transb) {

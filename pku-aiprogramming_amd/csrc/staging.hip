@@ -32,14 +32,8 @@
 namespace tt {
 namespace {
 
-#ifndef TT_STAGE_BUFS
-#define TT_STAGE_BUFS 3
-#endif
-#ifndef TT_STAGE_CHUNK_MIB
-#define TT_STAGE_CHUNK_MIB 16
-#endif
-constexpr int kBufs = TT_STAGE_BUFS;                          // pinned buffers in the ring
-constexpr size_t kChunk = size_t(TT_STAGE_CHUNK_MIB) << 20;  // bytes of one pinned buffer
+constexpr int kBufs = 3;                     // pinned buffers in the ring
+constexpr size_t kChunk = size_t(16) << 20;  // bytes of one pinned buffer
 constexpr size_t kRamp = size_t(1) << 20;        // first and last chunk bytes
 constexpr size_t kPiece = size_t(256) << 10;     // least device bytes per thread
 constexpr size_t kDirectMax = size_t(4) << 20;   // plain copies below this skip staging
