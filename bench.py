@@ -50,7 +50,6 @@ C4 = dict(B=64, H=32, Lkv=8192, d=128)
 # profiles/hbm_traffic_c5_c4.md.  Re-measured whenever a kernel changes.
 MEASURED_TRAFFIC_MIB = {
     "attn_fwd": 580.7,
-    "attn_bwd_delta": 264.0,
     "attn_decode_split": 8209.1,
     "softmax_reg": 2048.1,
     "gemm_bf16_nn": 2527.8 + 149.6,  # k_gemm_dma 8192^3 NN (profiles/gemm_kernel_stats.md)     # k_softmax_reg<16>, 262144 x 1024 fp32 (profiles/softmax_rows_kernel_stats.md)
@@ -70,7 +69,7 @@ def fwdbwd_flops(B, H, L, d, causal=True):
 def kernel_flops(B, H, L, d):
     """Algorithmic FLOPs each kernel of the step is charged with (causal)."""
     u = 2.0 * B * H * L * L * d / 2  # one L x L x d GEMM under the causal mask
-    return {"attn_fwd": 2 * u, "attn_bwd_dkdv": 3 * u, "attn_bwd_dq": 1 * u, "attn_bwd_delta": 0.0}
+    return {"attn_fwd": 2 * u, "attn_bwd_dq": 1 * u, "attn_bwd_dkdv": 3 * u}
 
 
 def decode_bytes(B, H, Lkv, d):
@@ -95,7 +94,9 @@ def run_fwdbwd(T, steps, warmup):
         step()
     T.lib().sync()
 
-    names = ["attn_fwd", "attn_bwd_delta", "attn_bwd_dkdv", "attn_bwd_dq"]
+    # launch order of one step: the forward, then the backward's dQ kernel (which
+    # also writes the rows -D and LSE log2(e)), then its dK/dV kernel
+    names = ["attn_fwd", "attn_bwd_dq", "attn_bwd_dkdv"]
     marks = [[T.Event() for _ in range(len(names) + 1)] for _ in range(steps)]
     start, stop = T.Event(), T.Event()
     T.lib().sync()

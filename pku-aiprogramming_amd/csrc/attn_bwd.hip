@@ -508,17 +508,23 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dq_bf1
 // so the exponentials of one block run on the VALU while the matrix cores
 // compute the next block's scores.  Barrier n makes tile n + 1 visible to
 // every wave and retires every read of tile n - 1, whose buffer then takes
-// tile n + 3: each tile gets two iterations of load lead.  The loop is
-// unrolled by the ring depth, so every LDS operand address is a
-// loop-invariant lane offset plus an immediate.
+// tile n + 3 (two iterations of load lead).  The loop is unrolled by the
+// ring depth, so every LDS operand address is a loop-invariant lane offset
+// plus an immediate.
+//
+// This kernel runs first in the backward and also does the row pre-pass the
+// dK/dV kernel needs: each lane forms D = sum_d dO o O of its query row from
+// the dO it holds and one read of O (the other half of the row is in lane
+// l ^ 32), and stores -D and LSE * log2(e) for the dK/dV kernel.
 constexpr int DQP_BN = 32;     // keys per block / LDS tile
 constexpr int DQP_STAGES = 4;  // LDS ring depth (the unrolled loop relies on it)
 
 template <int D, bool CAUSAL>
 __global__ __launch_bounds__(256, 2) void attn_bwd_dq_pipe_kernel(
     const u16* __restrict__ Q, const u16* __restrict__ K, const u16* __restrict__ V,
-    const u16* __restrict__ dO, const float* __restrict__ L2, const float* __restrict__ NDelta,
-    u16* __restrict__ dQ, int Lq, int Lk, int BH, int nqt, int group, float sl2, float scale) {
+    const u16* __restrict__ O, const u16* __restrict__ dO, const float* __restrict__ LSE,
+    float* __restrict__ L2, float* __restrict__ NDelta, u16* __restrict__ dQ, int Lq, int Lk, int BH, int nqt,
+    int group, float sl2, float scale) {
   using Tile = SwzTile<D>;
   constexpr int NW = 4, BM = 32 * NW, BN = DQP_BN, S = DQP_STAGES;
   constexpr int NC = D / 16, ND = D / 32;
@@ -537,17 +543,29 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_pipe_kernel(
   const int64_t kbase = (int64_t)bh * Lk * D;
 
   bf16x8 qf[NC], dof[NC];
+  float lse2, ndl;
   {
     const int qr = min(qrow, Lq - 1);  // padding rows read a valid row; never written back
+    float dsum = 0.f;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      qf[c] = __builtin_bit_cast(bf16x8, ldg16(Q + qbase + (int64_t)qr * D + 16 * c + 8 * g));
-      dof[c] = __builtin_bit_cast(bf16x8, ldg16(dO + qbase + (int64_t)qr * D + 16 * c + 8 * g));
+      const int64_t at = qbase + (int64_t)qr * D + 16 * c + 8 * g;
+      qf[c] = __builtin_bit_cast(bf16x8, ldg16(Q + at));
+      dof[c] = __builtin_bit_cast(bf16x8, ldg16(dO + at));
+      const bf16x8 of = __builtin_bit_cast(bf16x8, ldg16(O + at));
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dsum = fmaf((float)dof[c][e], (float)of[e], dsum);
+    }
+    dsum = sum_xor32(dsum);  // + the other half of the row (lane l ^ 32)
+    const int64_t row = (int64_t)bh * Lq + qrow;
+    // padding query rows: P = 2^(s - inf) = 0
+    lse2 = qrow < Lq ? LSE[(int64_t)bh * Lq + qr] * kLog2e : INFINITY;
+    ndl = qrow < Lq ? -dsum : 0.f;
+    if (g == 0 && qrow < Lq) {
+      NDelta[row] = ndl;
+      L2[row] = lse2;
     }
   }
-  // padding query rows: P = 2^(s - inf) = 0
-  const float lse2 = qrow < Lq ? L2[(int64_t)bh * Lq + qrow] : INFINITY;
-  const float ndl = qrow < Lq ? NDelta[(int64_t)bh * Lq + qrow] : 0.f;
   f32x16 adq[ND];
 #pragma unroll
   for (int dt = 0; dt < ND; ++dt) adq[dt] = f32x16{};
@@ -575,6 +593,15 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_pipe_kernel(
       tidx[1][dt] = Tile::at4(trow + 8, 32 * dt + tcol);
     }
   }
+
+  Dma dma;
+  dma.init();
+  int issued = 0;
+  auto issue_tile = [&](int n) {  // tile n into ring buffer n % S (n < ntiles)
+    u16* dst = smem + 2 * (n % S) * TE;
+    dma.issue(K + kbase, BN * n, Lk, dst);
+    dma.issue(V + kbase, BN * n, Lk, dst + TE);
+  };
 
   // S^T and dP^T of the block in ring buffer B
   auto sdp = [&](auto b_tag, f32x16& s, f32x16& dp) __attribute__((always_inline)) {
@@ -612,18 +639,10 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_pipe_kernel(
         adq[dt] = mfma_bf16_32x32x16(a, db[h], adq[dt]);
       }
   };
-
-  Dma dma;
-  dma.init();
-  int issued = 0;
-  auto issue_tile = [&](int n) {  // tile n into ring buffer n % S (n < ntiles)
-    u16* dst = smem + 2 * (n % S) * TE;
-    dma.issue(K + kbase, BN * n, Lk, dst);
-    dma.issue(V + kbase, BN * n, Lk, dst + TE);
-  };
   // Barrier n: this wave's loads of tile n + 1 have landed (loads retire in
   // issue order), then every wave's are visible and tile n - 1 is retired;
-  // tile n + S - 1 goes into its buffer.
+  // tile n + S - 1 goes into its buffer.  (Spreading these loads over the
+  // score MFMAs instead measured 9 % more cycles.)
   auto barrier_n = [&](int n) __attribute__((always_inline)) {
     const int ahead = issued - n - 2;
     wait_vmem_tiles<PER, S - 2>(ahead > 0 ? ahead : 0);
@@ -635,7 +654,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_pipe_kernel(
   };
 
   for (; issued < S - 1 && issued < ntiles; ++issued) issue_tile(issued);
-  wait_vmem_le<0>();  // also retires the Q / dO / LSE / D loads before the loop
+  wait_vmem_le<0>();  // also retires the Q / dO / O / LSE loads before the loop
   __syncthreads();
 
   using B0 = std::integral_constant<int, 0>;
@@ -662,16 +681,18 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_pipe_kernel(
   if (rem >= 1) it(n, B0{}, sA, pA, sB, pB);
   if (rem >= 2) it(n + 1, B1{}, sB, pB, sA, pA);
   if (rem >= 3) it(n + 2, B2{}, sA, pA, sB, pB);
-  barrier_n(last);
-  switch (rem) {
-    case 0: dsq(B0{}, sA, pA, BN * last, std::true_type{}); break;
-    case 1: dsq(B1{}, sB, pB, BN * last, std::true_type{}); break;
-    case 2: dsq(B2{}, sA, pA, BN * last, std::true_type{}); break;
-    default: dsq(B3{}, sB, pB, BN * last, std::true_type{}); break;
+  // the last block, then the barriers and loads of the later waves' blocks
+  for (int m = last; m < ntiles; ++m) {
+    barrier_n(m);
+    if (m == last) {
+      switch (rem) {
+        case 0: dsq(B0{}, sA, pA, BN * last, std::true_type{}); break;
+        case 1: dsq(B1{}, sB, pB, BN * last, std::true_type{}); break;
+        case 2: dsq(B2{}, sA, pA, BN * last, std::true_type{}); break;
+        default: dsq(B3{}, sB, pB, BN * last, std::true_type{}); break;
+      }
+    }
   }
-  // later tiles belong to other waves of the workgroup: take part in their
-  // barriers and loads
-  for (int m = last + 1; m < ntiles; ++m) barrier_n(m);
   wait_vmem_le<0>();  // nothing may be in flight into LDS when the workgroup exits
 
   if (qrow < Lq) {
@@ -698,6 +719,22 @@ static int launch_bwd(const T* q, const T* k, const T* v, const T* o, const floa
   constexpr bool BF = sizeof(T) == 2;
   const int64_t rows = BH * Lq;
   float* l2 = delta + rows;
+  const float sl2 = scale * kLog2e;
+  if constexpr (BF && D >= 64) {
+    // dQ first: it also writes -D and LSE * log2(e) for the dK/dV kernel
+    constexpr int NW = bwd_nw(D);
+    const int64_t nkt = (Lk + 32 * NW - 1) / (32 * NW);
+    const int64_t nqp = (Lq + 127) / 128;
+    if (nkt * BH > 0x7fffffff || nqp * BH > 0x7fffffff) return fail(TT_ERR_ARG, "attention backward: grid too large");
+    const int gp = pick_group(BH, nqp, 32 * 2), gk = pick_group(BH, nkt, 32 * 8 / NW);
+    hipLaunchKernelGGL((attn_bwd_dq_pipe_kernel<D, CAUSAL>), dim3((unsigned)(nqp * BH)), dim3(256), 0, st, q, k, v, o,
+                       dout, lse, l2, delta, dq, (int)Lq, (int)Lk, (int)BH, (int)nqp, gp, sl2, scale);
+    TT_LAUNCHED("attention backward dQ launch", st);
+    hipLaunchKernelGGL((attn_bwd_dkdv_bf16_kernel<D, CAUSAL>), dim3((unsigned)(nkt * BH)), dim3(64 * NW), 0, st, q,
+                       k, v, dout, l2, delta, dk, dv, (int)Lq, (int)Lk, (int)BH, (int)nkt, gk, sl2, scale);
+    TT_LAUNCHED("attention backward dK/dV launch", st);
+    return ok();
+  }
   constexpr int TPR = D / (16 / (int)sizeof(T));
   const int64_t dblk = (rows + (256 / TPR) - 1) / (256 / TPR);
   if (dblk > 0x7fffffff) return fail(TT_ERR_ARG, "attention backward: grid too large");
@@ -705,7 +742,6 @@ static int launch_bwd(const T* q, const T* k, const T* v, const T* o, const floa
                      l2, rows);
   TT_LAUNCHED("attention backward delta launch", st);
 
-  const float sl2 = scale * kLog2e;
   if constexpr (BF) {
     constexpr int NW = bwd_nw(D);
     const int64_t nkt = (Lk + 32 * NW - 1) / (32 * NW);
@@ -716,15 +752,8 @@ static int launch_bwd(const T* q, const T* k, const T* v, const T* o, const floa
     hipLaunchKernelGGL((attn_bwd_dkdv_bf16_kernel<D, CAUSAL>), dim3((unsigned)(nkt * BH)), dim3(64 * NW), 0, st, q,
                        k, v, dout, l2, delta, dk, dv, (int)Lq, (int)Lk, (int)BH, (int)nkt, gk, sl2, scale);
     TT_LAUNCHED("attention backward dK/dV launch", st);
-    if constexpr (D >= 64) {
-      const int64_t nqp = (Lq + 127) / 128;
-      const int gp = pick_group(BH, nqp, 32 * 2);
-      hipLaunchKernelGGL((attn_bwd_dq_pipe_kernel<D, CAUSAL>), dim3((unsigned)(nqp * BH)), dim3(256), 0, st, q, k, v,
-                         dout, l2, delta, dq, (int)Lq, (int)Lk, (int)BH, (int)nqp, gp, sl2, scale);
-    } else {
-      hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<D, CAUSAL>), dim3((unsigned)(nqt * BH)), dim3(64 * NW), 0, st,
-                         q, k, v, dout, l2, delta, dq, (int)Lq, (int)Lk, (int)BH, (int)nqt, gq, sl2, scale);
-    }
+    hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<D, CAUSAL>), dim3((unsigned)(nqt * BH)), dim3(64 * NW), 0, st, q, k,
+                       v, dout, l2, delta, dq, (int)Lq, (int)Lk, (int)BH, (int)nqt, gq, sl2, scale);
     TT_LAUNCHED("attention backward dQ launch", st);
   } else {
     const int64_t nkt = (Lk + BWD_F32_BN - 1) / BWD_F32_BN;
