@@ -293,6 +293,9 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_b
     }
     opaque(lofs);
     opaque(kofs);
+    // LLVM's single-wave MFMA / LDS interleave strategy for the tile's
+    // scheduling region (1 % fewer cycles at d = 128)
+    __builtin_amdgcn_iglp_opt(1);
     step(qb, b * 2 * TE, b * 4 * VS, mask_tag);
   };
   using AnyBuf = std::integral_constant<int, -1>;
@@ -667,6 +670,9 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_pipe_kernel(
   auto it = [&](int n, auto b_tag, f32x16& sc, f32x16& pc, f32x16& sn, f32x16& pn) __attribute__((always_inline)) {
     constexpr int B = decltype(b_tag)::value;
     barrier_n(n);
+    // LLVM's MFMA / exponential interleave strategy for the scheduling
+    // region of this iteration (2.5 % fewer cycles at d = 128)
+    __builtin_amdgcn_iglp_opt(2);
     sdp(std::integral_constant<int, (B + 1) % 4>{}, sn, pn);
     dsq(b_tag, sc, pc, BN * n, std::false_type{});
   };
@@ -733,39 +739,39 @@ static int launch_bwd(const T* q, const T* k, const T* v, const T* o, const floa
     hipLaunchKernelGGL((attn_bwd_dkdv_bf16_kernel<D, CAUSAL>), dim3((unsigned)(nkt * BH)), dim3(64 * NW), 0, st, q,
                        k, v, dout, l2, delta, dk, dv, (int)Lq, (int)Lk, (int)BH, (int)nkt, gk, sl2, scale);
     TT_LAUNCHED("attention backward dK/dV launch", st);
-    return ok();
-  }
-  constexpr int TPR = D / (16 / (int)sizeof(T));
-  const int64_t dblk = (rows + (256 / TPR) - 1) / (256 / TPR);
-  if (dblk > 0x7fffffff) return fail(TT_ERR_ARG, "attention backward: grid too large");
-  hipLaunchKernelGGL((attn_bwd_delta_kernel<T, D>), dim3((unsigned)dblk), dim3(256), 0, st, o, dout, lse, delta,
-                     l2, rows);
-  TT_LAUNCHED("attention backward delta launch", st);
-
-  if constexpr (BF) {
-    constexpr int NW = bwd_nw(D);
-    const int64_t nkt = (Lk + 32 * NW - 1) / (32 * NW);
-    const int64_t nqt = (Lq + 32 * NW - 1) / (32 * NW);
-    if (nkt * BH > 0x7fffffff || nqt * BH > 0x7fffffff) return fail(TT_ERR_ARG, "attention backward: grid too large");
-    // heads in flight per XCD: tiles for the resident workgroups of its 32 CUs
-    const int gk = pick_group(BH, nkt, 32 * 8 / NW), gq = pick_group(BH, nqt, 32 * 8 / NW);
-    hipLaunchKernelGGL((attn_bwd_dkdv_bf16_kernel<D, CAUSAL>), dim3((unsigned)(nkt * BH)), dim3(64 * NW), 0, st, q,
-                       k, v, dout, l2, delta, dk, dv, (int)Lq, (int)Lk, (int)BH, (int)nkt, gk, sl2, scale);
-    TT_LAUNCHED("attention backward dK/dV launch", st);
-    hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<D, CAUSAL>), dim3((unsigned)(nqt * BH)), dim3(64 * NW), 0, st, q, k,
-                       v, dout, l2, delta, dq, (int)Lq, (int)Lk, (int)BH, (int)nqt, gq, sl2, scale);
-    TT_LAUNCHED("attention backward dQ launch", st);
   } else {
-    const int64_t nkt = (Lk + BWD_F32_BN - 1) / BWD_F32_BN;
-    const int64_t nqt = (Lq + BWD_F32_BM - 1) / BWD_F32_BM;
-    if (nkt * BH > 0x7fffffff || nqt * BH > 0x7fffffff) return fail(TT_ERR_ARG, "attention backward: grid too large");
-    const int gk = pick_group(BH, nkt, 32), gq = pick_group(BH, nqt, 32);
-    hipLaunchKernelGGL((attn_bwd_dkdv_f32_kernel<D, CAUSAL>), dim3((unsigned)(nkt * BH)), dim3(256), 0, st,
-                       q, k, v, dout, lse, delta, dk, dv, (int)Lq, (int)Lk, (int)BH, (int)nkt, gk, sl2, scale);
-    TT_LAUNCHED("attention backward dK/dV launch", st);
-    hipLaunchKernelGGL((attn_bwd_dq_f32_kernel<D, CAUSAL>), dim3((unsigned)(nqt * BH)), dim3(256), 0, st,
-                       q, k, v, dout, lse, delta, dq, (int)Lq, (int)Lk, (int)BH, (int)nqt, gq, sl2, scale);
-    TT_LAUNCHED("attention backward dQ launch", st);
+    constexpr int TPR = D / (16 / (int)sizeof(T));
+    const int64_t dblk = (rows + (256 / TPR) - 1) / (256 / TPR);
+    if (dblk > 0x7fffffff) return fail(TT_ERR_ARG, "attention backward: grid too large");
+    hipLaunchKernelGGL((attn_bwd_delta_kernel<T, D>), dim3((unsigned)dblk), dim3(256), 0, st, o, dout, lse, delta,
+                       l2, rows);
+    TT_LAUNCHED("attention backward delta launch", st);
+
+    if constexpr (BF) {
+      constexpr int NW = bwd_nw(D);
+      const int64_t nkt = (Lk + 32 * NW - 1) / (32 * NW);
+      const int64_t nqt = (Lq + 32 * NW - 1) / (32 * NW);
+      if (nkt * BH > 0x7fffffff || nqt * BH > 0x7fffffff) return fail(TT_ERR_ARG, "attention backward: grid too large");
+      // heads in flight per XCD: tiles for the resident workgroups of its 32 CUs
+      const int gk = pick_group(BH, nkt, 32 * 8 / NW), gq = pick_group(BH, nqt, 32 * 8 / NW);
+      hipLaunchKernelGGL((attn_bwd_dkdv_bf16_kernel<D, CAUSAL>), dim3((unsigned)(nkt * BH)), dim3(64 * NW), 0, st, q,
+                         k, v, dout, l2, delta, dk, dv, (int)Lq, (int)Lk, (int)BH, (int)nkt, gk, sl2, scale);
+      TT_LAUNCHED("attention backward dK/dV launch", st);
+      hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<D, CAUSAL>), dim3((unsigned)(nqt * BH)), dim3(64 * NW), 0, st, q, k,
+                         v, dout, l2, delta, dq, (int)Lq, (int)Lk, (int)BH, (int)nqt, gq, sl2, scale);
+      TT_LAUNCHED("attention backward dQ launch", st);
+    } else {
+      const int64_t nkt = (Lk + BWD_F32_BN - 1) / BWD_F32_BN;
+      const int64_t nqt = (Lq + BWD_F32_BM - 1) / BWD_F32_BM;
+      if (nkt * BH > 0x7fffffff || nqt * BH > 0x7fffffff) return fail(TT_ERR_ARG, "attention backward: grid too large");
+      const int gk = pick_group(BH, nkt, 32), gq = pick_group(BH, nqt, 32);
+      hipLaunchKernelGGL((attn_bwd_dkdv_f32_kernel<D, CAUSAL>), dim3((unsigned)(nkt * BH)), dim3(256), 0, st,
+                         q, k, v, dout, lse, delta, dk, dv, (int)Lq, (int)Lk, (int)BH, (int)nkt, gk, sl2, scale);
+      TT_LAUNCHED("attention backward dK/dV launch", st);
+      hipLaunchKernelGGL((attn_bwd_dq_f32_kernel<D, CAUSAL>), dim3((unsigned)(nqt * BH)), dim3(256), 0, st,
+                         q, k, v, dout, lse, delta, dq, (int)Lq, (int)Lk, (int)BH, (int)nqt, gq, sl2, scale);
+      TT_LAUNCHED("attention backward dQ launch", st);
+    }
   }
   return ok();
 }

@@ -437,6 +437,9 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fwd_bf16_pipe_kernel(
     // the rare O rescale goes first, so that both phases form one basic
     // block for the scheduler
     if (rescale) rescale_o();
+    // LLVM's MFMA / transcendental interleave strategy for this block: one
+    // v_exp_f32 between consecutive MFMAs (2.5 % fewer cycles at d = 128)
+    __builtin_amdgcn_iglp_opt(3);
     if constexpr (SPREAD)
       qk(sK + kbuf * TE, nx, load_kv);
     else
@@ -488,10 +491,9 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fwd_bf16_pipe_kernel(
     ++j;
   }
   if (last >= 1) {
-    if (mask_last)
-      body(j, sa, sb, std::true_type{}, Any{}, std::false_type{});
-    else
-      body(j, sa, sb, std::false_type{}, Any{}, std::false_type{});
+    // always the masking body: a second copy for unmasked last tiles made the
+    // non-causal d = 128 kernel spill a Q fragment inside its main loop
+    body(j, sa, sb, std::true_type{}, Any{}, std::false_type{});
     sa[0] = sb[0];
     sa[1] = sb[1];
   }
