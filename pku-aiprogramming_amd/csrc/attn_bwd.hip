@@ -763,14 +763,12 @@ static int launch_bwd(const T* q, const T* k, const T* v, const T* o, const floa
     } else {
       const int64_t nkt = (Lk + BWD_F32_BN - 1) / BWD_F32_BN;
       const int64_t nqt = (Lq + BWD_F32_BM - 1) / BWD_F32_BM;
-      if (nkt * BH > 0x7fffffff || nqt * BH > 0x7fffffff) return fail(TT_ERR_ARG, "attention backward: grid too large");
+      if ((nkt + nqt) * BH > 0x7fffffff) return fail(TT_ERR_ARG, "attention backward: grid too large");
       const int gk = pick_group(BH, nkt, 32), gq = pick_group(BH, nqt, 32);
-      hipLaunchKernelGGL((attn_bwd_dkdv_f32_kernel<D, CAUSAL>), dim3((unsigned)(nkt * BH)), dim3(256), 0, st,
-                         q, k, v, dout, lse, delta, dk, dv, (int)Lq, (int)Lk, (int)BH, (int)nkt, gk, sl2, scale);
-      TT_LAUNCHED("attention backward dK/dV launch", st);
-      hipLaunchKernelGGL((attn_bwd_dq_f32_kernel<D, CAUSAL>), dim3((unsigned)(nqt * BH)), dim3(256), 0, st,
-                         q, k, v, dout, lse, delta, dq, (int)Lq, (int)Lk, (int)BH, (int)nqt, gq, sl2, scale);
-      TT_LAUNCHED("attention backward dQ launch", st);
+      hipLaunchKernelGGL((attn_bwd_f32_kernel<D, CAUSAL>), dim3((unsigned)((nkt + nqt) * BH)), dim3(256), 0, st,
+                         q, k, v, dout, lse, delta, dq, dk, dv, (int)Lq, (int)Lk, (int)BH, (int)nkt, (int)nqt,
+                         (int)(nkt * BH), gk, gq, sl2, scale);
+      TT_LAUNCHED("attention backward dQ / dK / dV launch", st);
     }
   }
   return ok();

@@ -13,24 +13,33 @@ constexpr int BWD_F32_BQ = 64;   // queries per LDS step of the dK/dV kernel
 constexpr int BWD_F32_BM = 128;  // queries per dQ workgroup
 constexpr int BWD_F32_KN = 64;   // keys per LDS step of the dQ kernel
 
+// LDS floats of each role: Q and dO tiles plus their LSE / -D rows; K and V tiles.
+template <int D>
+constexpr int bwd_f32_dkdv_lds() { return 2 * BWD_F32_BQ * (D + 1) + 2 * BWD_F32_BQ; }
+template <int D>
+constexpr int bwd_f32_dq_lds() { return 2 * BWD_F32_KN * (D + 1); }
+
+// dK / dV of the BWD_F32_BN keys of tile `id` (see map_tile), looping over
+// the query tiles.
 template <int D, bool CAUSAL>
-__global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_f32_kernel(
-    const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
-    const float* __restrict__ dO, const float* __restrict__ LSE, const float* __restrict__ NDelta,
-    float* __restrict__ dK, float* __restrict__ dV, int Lq, int Lk, int BH, int nkt, int group,
-    float sl2, float scale) {
+__device__ __forceinline__ void bwd_f32_dkdv(int id, float* smem, const float* __restrict__ Q,
+                                             const float* __restrict__ K, const float* __restrict__ V,
+                                             const float* __restrict__ dO, const float* __restrict__ LSE,
+                                             const float* __restrict__ NDelta, float* __restrict__ dK,
+                                             float* __restrict__ dV, int Lq, int Lk, int BH, int nkt, int group,
+                                             float sl2, float scale) {
   constexpr int BN = BWD_F32_BN, BQ = BWD_F32_BQ;
   constexpr int P = D + 1;
   constexpr int NC = D / 2, ND = D / 32, CPR = D / 4;
   constexpr int LPT = BQ * CPR / 256;
-  __shared__ float sQ[BQ * P];
-  __shared__ float sdO[BQ * P];
-  __shared__ float sL[BQ];
-  __shared__ float sDl[BQ];
+  float* sQ = smem;
+  float* sdO = sQ + BQ * P;
+  float* sL = sdO + BQ * P;
+  float* sDl = sL + BQ;
 
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, g = l >> 5, r32 = l & 31;
   int kt, bh;
-  map_tile(blockIdx.x, nkt, BH, group, kt, bh, false);
+  map_tile(id, nkt, BH, group, kt, bh, false);
   const int k0 = kt * BN;
   const int key = k0 + 32 * w + r32;
   const int wk_lo = k0 + 32 * w;
@@ -136,22 +145,23 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_f32_kernel(
   }
 }
 
-// ------------------------------------------------------------------ fp32 dQ
+// dQ of the BWD_F32_BM queries of tile `id`, looping over the key tiles.
 template <int D, bool CAUSAL>
-__global__ __launch_bounds__(256, 1) void attn_bwd_dq_f32_kernel(
-    const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
-    const float* __restrict__ dO, const float* __restrict__ LSE, const float* __restrict__ NDelta,
-    float* __restrict__ dQ, int Lq, int Lk, int BH, int nqt, int group, float sl2, float scale) {
+__device__ __forceinline__ void bwd_f32_dq(int id, float* smem, const float* __restrict__ Q,
+                                           const float* __restrict__ K, const float* __restrict__ V,
+                                           const float* __restrict__ dO, const float* __restrict__ LSE,
+                                           const float* __restrict__ NDelta, float* __restrict__ dQ, int Lq,
+                                           int Lk, int BH, int nqt, int group, float sl2, float scale) {
   constexpr int BM = BWD_F32_BM, BN = BWD_F32_KN;
   constexpr int P = D + 1;
   constexpr int NC = D / 2, ND = D / 32, CPR = D / 4;
   constexpr int LPT = BN * CPR / 256;
-  __shared__ float sK[BN * P];
-  __shared__ float sV[BN * P];
+  float* sK = smem;
+  float* sV = sK + BN * P;
 
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, g = l >> 5, r32 = l & 31;
   int qt, bh;
-  map_tile(blockIdx.x, nqt, BH, group, qt, bh, CAUSAL);
+  map_tile(id, nqt, BH, group, qt, bh, CAUSAL);
   const int q0 = qt * BM;
   const int qrow = q0 + 32 * w + r32;
   const int wq_lo = q0 + 32 * w, wq_hi = wq_lo + 31;
@@ -240,6 +250,27 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_f32_kernel(
         *reinterpret_cast<float4*>(row + 32 * dt + acc_row(r, g)) = v;
       }
   }
+}
+
+// Both roles in one launch: workgroups [0, nkblk) compute dK / dV, the rest
+// dQ.  Each role alone puts one workgroup per key or query tile on the chip
+// (one wave per SIMD at these register counts), so a small problem fills
+// only part of the CUs with either; together they fill twice as many.
+// nkblk is nkt * BH, a multiple of 8 when BH is, so the dQ workgroups keep
+// their XCD mapping.
+template <int D, bool CAUSAL>
+__global__ __launch_bounds__(256, 1) void attn_bwd_f32_kernel(
+    const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
+    const float* __restrict__ dO, const float* __restrict__ LSE, const float* __restrict__ NDelta,
+    float* __restrict__ dQ, float* __restrict__ dK, float* __restrict__ dV, int Lq, int Lk, int BH, int nkt,
+    int nqt, int nkblk, int gk, int gq, float sl2, float scale) {
+  constexpr int kLds = bwd_f32_dkdv_lds<D>() > bwd_f32_dq_lds<D>() ? bwd_f32_dkdv_lds<D>() : bwd_f32_dq_lds<D>();
+  __shared__ float smem[kLds];
+  const int id = blockIdx.x;
+  if (id < nkblk)
+    bwd_f32_dkdv<D, CAUSAL>(id, smem, Q, K, V, dO, LSE, NDelta, dK, dV, Lq, Lk, BH, nkt, gk, sl2, scale);
+  else
+    bwd_f32_dq<D, CAUSAL>(id - nkblk, smem, Q, K, V, dO, LSE, NDelta, dQ, Lq, Lk, BH, nqt, gq, sl2, scale);
 }
 
 }  // namespace tt

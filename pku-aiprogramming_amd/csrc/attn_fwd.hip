@@ -526,11 +526,16 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fwd_bf16_pipe_kernel(
   }
 }
 
+// fp32 forward.  With nsplit > 1 the key range of each query tile is split
+// over nsplit workgroups (workgroup id = split * nqt * BH + tile id), each
+// writing its unnormalised O, running max and row sum to `part`; the combine
+// kernel below merges them.  Small problems (c2: 128 query tiles) then still
+// put a workgroup on every CU.
 template <int D, bool CAUSAL>
 __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void attn_fwd_f32_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     float* __restrict__ O, float* __restrict__ LSE, int Lq, int Lk, int BH, int nqt, int group,
-    float sl2) {
+    float sl2, int nsplit, float* __restrict__ part) {
   constexpr int BM = FWD_F32_BM, BN = FWD_BN;
   constexpr int P = D + 1;    // row pitch (floats): lanes on consecutive rows hit distinct banks
   constexpr int NC = D / 2;   // k-steps of the d contraction (2 per MFMA)
@@ -541,8 +546,10 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void attn_fwd_f32_kernel(
   __shared__ float sV[BN * P];
 
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, g = l >> 5, r32 = l & 31;
+  const int ntq = nqt * BH;
+  const int split = blockIdx.x / ntq;
   int qt, bh;
-  map_tile(blockIdx.x, nqt, BH, group, qt, bh, CAUSAL);
+  map_tile(blockIdx.x - split * ntq, nqt, BH, group, qt, bh, CAUSAL);
   const int q0 = qt * BM;
   const int qrow = q0 + 32 * w + r32;
   const int64_t qbase = (int64_t)bh * Lq * D;
@@ -559,7 +566,11 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void attn_fwd_f32_kernel(
 #pragma unroll
   for (int dt = 0; dt < ND; ++dt) acc[dt] = f32x16{};
   float m = -INFINITY, lsum = 0.f;
+  // this workgroup's key tiles: [kb_lo, kb_hi) of [0, kend), split `split`
+  // of nsplit equal runs of whole tiles (a run may be empty)
   const int kend = CAUSAL ? min(Lk, q0 + BM) : Lk;
+  const int per = ((kend + BN - 1) / BN + nsplit - 1) / nsplit * BN;
+  const int kb_lo = min(kend, split * per), kb_hi = min(kend, kb_lo + per);
   const int wq_lo = q0 + 32 * w, wq_hi = wq_lo + 31;
 
   float4 kreg[LPT], vreg[LPT];
@@ -584,12 +595,12 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void attn_fwd_f32_kernel(
     }
   };
 
-  if (kend > 0) gload(0);
-  for (int kb = 0; kb < kend; kb += BN) {
+  if (kb_lo < kb_hi) gload(kb_lo);
+  for (int kb = kb_lo; kb < kb_hi; kb += BN) {
     __syncthreads();
     sstore();
     __syncthreads();
-    if (kb + BN < kend) gload(kb + BN);
+    if (kb + BN < kb_hi) gload(kb + BN);
     if (CAUSAL && kb > wq_hi) continue;
 
     f32x16 s[2];
@@ -642,8 +653,9 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void attn_fwd_f32_kernel(
 
   lsum += wave_xor32(lsum);
   if (qrow < Lq) {
-    const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-    float* orow = O + qbase + (int64_t)qrow * D;
+    const int64_t row = (int64_t)bh * Lq + qrow;
+    const float inv = nsplit > 1 ? 1.f : (lsum > 0.f ? 1.f / lsum : 0.f);
+    float* orow = nsplit > 1 ? part + ((int64_t)split * BH * Lq + row) * D : O + qbase + (int64_t)qrow * D;
 #pragma unroll
     for (int dt = 0; dt < ND; ++dt)
 #pragma unroll
@@ -651,8 +663,49 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void attn_fwd_f32_kernel(
         float4 v = {acc[dt][r] * inv, acc[dt][r + 1] * inv, acc[dt][r + 2] * inv, acc[dt][r + 3] * inv};
         *reinterpret_cast<float4*>(orow + 32 * dt + acc_row(r, g)) = v;
       }
-    if (g == 0 && LSE) LSE[(int64_t)bh * Lq + qrow] = (m + __log2f(lsum)) * kLn2;
+    if (g == 0) {
+      if (nsplit > 1) {
+        float* ml = part + (int64_t)nsplit * BH * Lq * D + 2 * ((int64_t)split * BH * Lq + row);
+        ml[0] = m;
+        ml[1] = lsum;
+      } else if (LSE) {
+        LSE[row] = (m + __log2f(lsum)) * kLn2;
+      }
+    }
   }
+}
+
+// Merges the nsplit partial results of the split fp32 forward: per query
+// row, with M = max of the splits' running maxima, O = sum_s 2^(m_s - M) O_s /
+// sum_s 2^(m_s - M) l_s and LSE = (M + log2 of that denominator) ln 2.  A split
+// with no keys for the row has m_s = -inf and weight 0; split 0 always holds
+// key 0, which every query sees.  D / 4 threads per row, one float4 each.
+template <int D>
+__global__ __launch_bounds__(256) void attn_fwd_f32_combine_kernel(const float* __restrict__ part,
+                                                                   float* __restrict__ O, float* __restrict__ LSE,
+                                                                   int64_t rows, int nsplit) {
+  constexpr int TPR = D / 4;
+  const int64_t row = (int64_t)blockIdx.x * (256 / TPR) + threadIdx.x / TPR;
+  const int c = threadIdx.x % TPR;
+  if (row >= rows) return;
+  const float* ml = part + (int64_t)nsplit * rows * D;
+  float mx = -INFINITY;
+  for (int sp = 0; sp < nsplit; ++sp) mx = fmaxf(mx, ml[2 * (sp * rows + row)]);
+  float den = 0.f;
+  float4 num = {0.f, 0.f, 0.f, 0.f};
+  for (int sp = 0; sp < nsplit; ++sp) {
+    const int64_t pr = sp * rows + row;
+    const float wgt = fast_exp2(ml[2 * pr] - mx);  // 0 for an empty split (m = -inf)
+    den += wgt * ml[2 * pr + 1];
+    const float4 o = *reinterpret_cast<const float4*>(part + pr * D + 4 * c);
+    num.x += wgt * o.x;
+    num.y += wgt * o.y;
+    num.z += wgt * o.z;
+    num.w += wgt * o.w;
+  }
+  const float inv = den > 0.f ? 1.f / den : 0.f;
+  *reinterpret_cast<float4*>(O + row * D + 4 * c) = float4{num.x * inv, num.y * inv, num.z * inv, num.w * inv};
+  if (c == 0 && LSE) LSE[row] = (mx + __log2f(den)) * kLn2;
 }
 
 template <typename T, typename KernelPtr>
@@ -688,7 +741,39 @@ static int fwd_bf16(const u16* q, const u16* k, const u16* v, u16* o, float* lse
 template <int D, bool CAUSAL>
 static int fwd_f32(const float* q, const float* k, const float* v, float* o, float* lse, int64_t BH, int64_t Lq,
                    int64_t Lk, float scale, hipStream_t st) {
-  return launch_fwd(attn_fwd_f32_kernel<D, CAUSAL>, FWD_F32_BM, 256, 2, q, k, v, o, lse, BH, Lq, Lk, scale, st);
+  constexpr int wg_per_cu = D >= 128 ? 1 : 2;
+  const int64_t nqt = (Lq + FWD_F32_BM - 1) / FWD_F32_BM;
+  const int64_t ntq = nqt * BH;
+  // Split the keys when the query tiles alone leave CUs idle: up to 4 splits,
+  // each with at least one key tile.
+  const int64_t slots = 256 * wg_per_cu, ktiles = (Lk + FWD_BN - 1) / FWD_BN;
+  int64_t nsplit = ntq >= slots ? 1 : (slots + ntq - 1) / ntq;
+  if (nsplit > 4) nsplit = 4;
+  if (nsplit > ktiles) nsplit = ktiles;
+  if (nsplit < 1) nsplit = 1;
+  if (ntq * nsplit > 0x7fffffff) return fail(TT_ERR_ARG, "attention forward: grid too large");
+  const int group = pick_group(BH, nqt, 32 * wg_per_cu);
+  const float sl2 = scale * kLog2e;
+  if (nsplit == 1) {
+    hipLaunchKernelGGL((attn_fwd_f32_kernel<D, CAUSAL>), dim3((unsigned)ntq), dim3(256), 0, st, q, k, v, o, lse,
+                       (int)Lq, (int)Lk, (int)BH, (int)nqt, group, sl2, 1, nullptr);
+    TT_LAUNCHED("attention forward launch", st);
+    return ok();
+  }
+  const int64_t rows = BH * Lq;
+  void* ws = nullptr;
+  WorkspaceLease lease;  // held until both kernels are launched
+  int rc = lease.get(st, kWsForwardSplits, (size_t)(nsplit * rows) * (D + 2) * sizeof(float), &ws);
+  if (rc) return rc;
+  float* part = (float*)ws;
+  hipLaunchKernelGGL((attn_fwd_f32_kernel<D, CAUSAL>), dim3((unsigned)(ntq * nsplit)), dim3(256), 0, st, q, k, v,
+                     o, lse, (int)Lq, (int)Lk, (int)BH, (int)nqt, group, sl2, (int)nsplit, part);
+  TT_LAUNCHED("attention forward split launch", st);
+  constexpr int RPB = 256 / (D / 4);  // rows per combine workgroup
+  hipLaunchKernelGGL((attn_fwd_f32_combine_kernel<D>), dim3((unsigned)((rows + RPB - 1) / RPB)), dim3(256), 0, st,
+                     (const float*)part, o, lse, rows, (int)nsplit);
+  TT_LAUNCHED("attention forward combine launch", st);
+  return ok();
 }
 
 }  // namespace tt

@@ -36,7 +36,7 @@ void* noalloc_scratch(size_t* bytes);
 // grown on demand and kept for reuse.  A lease holds the workspace lock from
 // get() until it is destroyed: keep it alive until every kernel that reads
 // the buffer has been launched on that stream.
-enum { kWsBackwardRows = 0, kWsDecodePartials = 1 };
+enum { kWsBackwardRows = 0, kWsDecodePartials = 1, kWsForwardSplits = 2 };
 class WorkspaceLease {
  public:
   WorkspaceLease();
