@@ -147,8 +147,26 @@ def run_decode(T, steps, warmup):
     total_ms = T.Event.elapsed(start, stop)
     per = {n: sum(T.Event.elapsed(marks[s][i], marks[s][i + 1]) for s in range(steps)) / steps
            for i, n in enumerate(names)}
+    # The read rate this hardware gives a plain streaming kernel over the same
+    # K and V buffers (tt_read_probe: 16-byte loads, 256 KiB per workgroup).
+    L = T.lib()
+    sink = T.DeviceBuffer((1,), "f32")
+    for _ in range(warmup):
+        L.call("tt_read_probe", k.ptr, k.nbytes, sink.ptr, None)
+        L.call("tt_read_probe", v.ptr, v.nbytes, sink.ptr, None)
+    L.sync()
+    start.record()
+    for _ in range(steps):
+        L.call("tt_read_probe", k.ptr, k.nbytes, sink.ptr, None)
+        L.call("tt_read_probe", v.ptr, v.nbytes, sink.ptr, None)
+    stop.record()
+    L.sync()
+    probe_ms = T.Event.elapsed(start, stop) / steps
+    read_ceiling = {"value": (k.nbytes + v.nbytes) / (probe_ms * 1e-3) / 1e9, "unit": "GB/s",
+                    "ms": probe_ms, "bytes": k.nbytes + v.nbytes,
+                    "kernel": "k_read_probe (tt_read_probe over the K and V buffers)"}
     del k, v
-    return total_ms / steps, per
+    return total_ms / steps, per, read_ceiling
 
 
 # The other BASELINE.json configurations (parity configs c1-c3), each timed
@@ -584,7 +602,7 @@ def main(argv=None):
                            "algorithmic_flop_per_launch": kf[dom]}
 
     if args.only in ("all", "decode"):
-        ms, per = run_decode(T, args.steps, args.warmup)
+        ms, per, read_ceiling = run_decode(T, args.steps, args.warmup)
         nbytes = decode_bytes(**C4)
         gbs = nbytes / (ms * 1e-3) / 1e9
         split = per["attn_decode_split"]
@@ -597,6 +615,8 @@ def main(argv=None):
             "roofline": {"bound": "hbm", "kernel": "attn_decode_split", "achieved": sgbs, "peak": PEAK_HBM_GBS,
                          "unit": "GB/s", "frac": sgbs / PEAK_HBM_GBS, "traffic": traffic_bytes("attn_decode_split"),
                          "algorithmic_bytes_per_launch": split_bytes},
+            "read_ceiling": read_ceiling,
+            "frac_of_read_ceiling": sgbs / read_ceiling["value"],
         }
         if not args.no_cpu_baseline:
             out["decode"]["cpu_baseline"] = decode_cpu_baseline()

@@ -124,6 +124,14 @@ int tt_event_destroy(void* ev);
  * evs = NULL) disables it.  The events must stay alive until recorded. */
 int tt_set_launch_events(void** evs, int n);
 
+/* Benchmark instrumentation (no counterpart in the reference): streams
+ * `bytes` bytes of device memory at `buf` (16-byte aligned, bytes a multiple
+ * of 16) with 16-byte loads, one contiguous 256 KiB run per workgroup, and
+ * stores nothing (out, one float, is written only if the data sums to a
+ * sentinel).  It gives the HBM read rate that the decode kernel, which also
+ * streams K and V once, is compared against. */
+int tt_read_probe(const void* buf, int64_t bytes, float* out, void* stream);
+
 /* ------------------------------------------------------------ elementwise */
 
 /* Elementwise ops of TinyTensor (src/TinyTensor_kernels.cu:6-85).

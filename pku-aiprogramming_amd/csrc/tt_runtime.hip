@@ -393,6 +393,39 @@ int tt_set_launch_events(void** evs, int n) {
   return TT_OK;
 }
 
+// Streams chunk16 16-byte words per workgroup (workgroup b: words
+// [b * chunk16, min((b + 1) * chunk16, n16))), 16 loads in flight per thread.
+__global__ __launch_bounds__(256) void k_read_probe(const uint4* __restrict__ p, int64_t n16, int64_t chunk16,
+                                                     float* out) {
+  const int64_t lo = (int64_t)blockIdx.x * chunk16;
+  const int64_t hi = lo + chunk16 < n16 ? lo + chunk16 : n16;
+  float acc = 0.f;
+  for (int64_t i = lo + threadIdx.x; i < hi; i += 256 * 16) {
+    uint4 v[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) v[u] = i + 256 * u < hi ? p[i + 256 * u] : uint4{0, 0, 0, 0};
+#pragma unroll
+    for (int u = 0; u < 16; ++u)
+      acc += (__uint_as_float(v[u].x) + __uint_as_float(v[u].y)) + (__uint_as_float(v[u].z) + __uint_as_float(v[u].w));
+  }
+  if (acc == 1234.5f) out[0] = acc;  // keeps the loads; practically never taken
+}
+
+int tt_read_probe(const void* buf, int64_t bytes, float* out, void* stream) {
+  if (bytes < 0 || bytes % 16 != 0) return fail(TT_ERR_ARG, "tt_read_probe: bytes must be a multiple of 16");
+  if (bytes == 0) return TT_OK;
+  if (!buf || !out || ((uintptr_t)buf & 15)) return fail(TT_ERR_ARG, "tt_read_probe: null or unaligned pointer");
+  int rc = ensure_init();
+  if (rc) return rc;
+  const int64_t n16 = bytes / 16, chunk16 = (int64_t(256) << 10) / 16;
+  const int64_t nb = (n16 + chunk16 - 1) / chunk16;
+  if (nb > 0x7fffffff) return fail(TT_ERR_ARG, "tt_read_probe: too large");
+  hipStream_t s = stream_or_default(stream);
+  hipLaunchKernelGGL(k_read_probe, dim3((unsigned)nb), dim3(256), 0, s, (const uint4*)buf, n16, chunk16, out);
+  TT_LAUNCHED("read probe launch", s);
+  return ok();
+}
+
 int tt_elementwise(int op, int dtype, void* c, const void* a, const void* b, int64_t n,
                    double alpha, double beta, uint64_t seed, void* stream) {
   if (n < 0) return fail(TT_ERR_ARG, "tt_elementwise: negative size");

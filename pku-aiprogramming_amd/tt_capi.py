@@ -54,6 +54,7 @@ _SIGS = {
     "tt_event_elapsed_ms": (C.c_int, [C.POINTER(C.c_float), _p, _p]),
     "tt_event_destroy": (C.c_int, [_p]),
     "tt_set_launch_events": (C.c_int, [C.POINTER(_p), C.c_int]),
+    "tt_read_probe": (C.c_int, [_p, _i64, _p, _p]),
     "tt_elementwise": (C.c_int, [C.c_int, C.c_int, _p, _p, _p, _i64, C.c_double, C.c_double, C.c_uint64, _p]),
     "tt_fill_normal": (C.c_int, [C.c_int, _p, _i64, C.c_uint64, C.c_float, _p]),
     "tt_attn_fwd_f32": (C.c_int, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, C.c_float, C.c_int, _p]),

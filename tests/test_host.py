@@ -84,6 +84,12 @@ def test_argument_errors_need_no_gpu(capi):
     assert sm(None, None, 2, 4, None) == capi.TT_ERR_ARG and "null pointer" in L.last_error()
     assert sm(None, None, 0, 4, None) == capi.TT_OK
     assert sm(None, None, 3, 0, None) == capi.TT_OK
+    # read probe: sizes that are not whole 16-byte words, null / unaligned buffers, empty work
+    rp = L.lib.tt_read_probe
+    assert rp(None, 24, None, None) == capi.TT_ERR_ARG and "multiple of 16" in L.last_error()
+    assert rp(None, 32, None, None) == capi.TT_ERR_ARG and "null" in L.last_error()
+    assert rp(C.c_void_p(8), 32, C.c_void_p(64), None) == capi.TT_ERR_ARG and "unaligned" in L.last_error()
+    assert rp(None, 0, None, None) == capi.TT_OK
 
 
 @pytest.mark.skipif(_gpu_present(), reason="checks the no-device path")

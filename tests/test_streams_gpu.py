@@ -142,3 +142,16 @@ def test_allocation_failure_injection(capi):
                        capture_output=True, text=True, timeout=120, env=env)
     _say(r.stdout[-500:] + r.stderr[-2000:])
     assert r.returncode == 0 and "CHILD_OK" in r.stdout
+
+
+def test_read_probe_reads_and_stores_nothing(capi):
+    """The bench's read-rate probe: a ragged size (not a whole number of
+    256 KiB runs) runs without error and leaves its sink alone (zero data
+    never sums to the sentinel)."""
+    L = capi.lib()
+    buf = capi.DeviceBuffer(((1 << 18) + 12,), "f32")  # 1 MiB + 48 bytes
+    buf.zero()
+    sink = capi.DeviceBuffer.from_numpy(np.array([7.0], dtype=np.float32), "f32")
+    L.check(L.lib.tt_read_probe(buf.ptr, buf.nbytes, sink.ptr, None), "tt_read_probe")
+    L.sync()
+    assert sink.download()[0] == 7.0
