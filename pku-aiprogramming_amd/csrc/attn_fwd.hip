@@ -537,13 +537,18 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void attn_fwd_f32_kernel(
     float* __restrict__ O, float* __restrict__ LSE, int Lq, int Lk, int BH, int nqt, int group,
     float sl2, int nsplit, float* __restrict__ part) {
   constexpr int BM = FWD_F32_BM, BN = FWD_BN;
-  constexpr int P = D + 1;    // row pitch (floats): lanes on consecutive rows hit distinct banks
   constexpr int NC = D / 2;   // k-steps of the d contraction (2 per MFMA)
   constexpr int ND = D / 32;
   constexpr int CPR = D / 4;  // 16-byte chunks per row
   constexpr int LPT = BN * CPR / 256;
-  __shared__ float sK[BN * P];
-  __shared__ float sV[BN * P];
+  // K rows with d-index k at column (k & 1) * D/2 + k/2, so that the k-values
+  // 2c + g of consecutive MFMAs are adjacent for lane half g (one 16-byte read
+  // feeds four MFMAs); V stored transposed, sV[d][key], so that the four keys
+  // of four consecutive accumulator rows are adjacent.  Row pitches of 4 mod
+  // 64 floats put the 16 rows of a 16-lane read pass on distinct banks.
+  constexpr int PK = D + 4, PV = BN + 4;
+  __shared__ __align__(16) float sK[BN * PK];
+  __shared__ __align__(16) float sV[D * PV];
 
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, g = l >> 5, r32 = l & 31;
   const int ntq = nqt * BH;
@@ -587,11 +592,15 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void attn_fwd_f32_kernel(
 #pragma unroll
     for (int i = 0; i < LPT; ++i) {
       const int c = tid + 256 * i;
-      const int key = c / CPR, ch = c % CPR;
-      float* pk = &sK[key * P + 4 * ch];
-      float* pv = &sV[key * P + 4 * ch];
-      pk[0] = kreg[i].x; pk[1] = kreg[i].y; pk[2] = kreg[i].z; pk[3] = kreg[i].w;
-      pv[0] = vreg[i].x; pv[1] = vreg[i].y; pv[2] = vreg[i].z; pv[3] = vreg[i].w;
+      const int key = c / CPR, ch = c % CPR;  // d-indices 4ch .. 4ch + 3
+      float* pk = &sK[key * PK + 2 * ch];
+      *reinterpret_cast<float2*>(pk) = float2{kreg[i].x, kreg[i].z};          // even k
+      *reinterpret_cast<float2*>(pk + D / 2) = float2{kreg[i].y, kreg[i].w};  // odd k
+      float* pv = &sV[4 * ch * PV + key];
+      pv[0] = vreg[i].x;
+      pv[PV] = vreg[i].y;
+      pv[2 * PV] = vreg[i].z;
+      pv[3 * PV] = vreg[i].w;
     }
   };
 
@@ -607,8 +616,15 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void attn_fwd_f32_kernel(
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       s[t] = f32x16{};
+      const float* kr = &sK[(32 * t + r32) * PK + g * (D / 2)];
 #pragma unroll
-      for (int c = 0; c < NC; ++c) s[t] = mfma_f32_32x32x2(sK[(32 * t + r32) * P + 2 * c + g], qf[c], s[t]);
+      for (int c4 = 0; c4 < NC / 4; ++c4) {
+        const float4 kk = *reinterpret_cast<const float4*>(kr + 4 * c4);
+        s[t] = mfma_f32_32x32x2(kk.x, qf[4 * c4], s[t]);
+        s[t] = mfma_f32_32x32x2(kk.y, qf[4 * c4 + 1], s[t]);
+        s[t] = mfma_f32_32x32x2(kk.z, qf[4 * c4 + 2], s[t]);
+        s[t] = mfma_f32_32x32x2(kk.w, qf[4 * c4 + 3], s[t]);
+      }
     }
     const bool need_mask = (kb + BN > Lk) || (CAUSAL && kb + BN - 1 > wq_lo);
     float mx = -INFINITY;
@@ -641,14 +657,21 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void attn_fwd_f32_kernel(
     lsum = lsum * alpha + ps;
 #pragma unroll
     for (int dt = 0; dt < ND; ++dt) acc[dt] *= alpha;
-    // O^T += V^T P^T, two keys (one per lane half) per MFMA.
+    // O^T += V^T P^T, two keys (one per lane half) per MFMA: accumulator
+    // rows 4j .. 4j + 3 of lane half g are keys 32t + 8j + 4g + 0..3, one
+    // 16-byte read of the transposed V tile.
 #pragma unroll
     for (int dt = 0; dt < ND; ++dt)
 #pragma unroll
       for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-          acc[dt] = mfma_f32_32x32x2(sV[(32 * t + acc_row(r, g)) * P + 32 * dt + r32], s[t][r], acc[dt]);
+        for (int j = 0; j < 4; ++j) {
+          const float4 vv = *reinterpret_cast<const float4*>(&sV[(32 * dt + r32) * PV + 32 * t + 8 * j + 4 * g]);
+          acc[dt] = mfma_f32_32x32x2(vv.x, s[t][4 * j], acc[dt]);
+          acc[dt] = mfma_f32_32x32x2(vv.y, s[t][4 * j + 1], acc[dt]);
+          acc[dt] = mfma_f32_32x32x2(vv.z, s[t][4 * j + 2], acc[dt]);
+          acc[dt] = mfma_f32_32x32x2(vv.w, s[t][4 * j + 3], acc[dt]);
+        }
   }
 
   lsum += wave_xor32(lsum);
