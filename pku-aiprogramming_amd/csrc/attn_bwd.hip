@@ -6,7 +6,7 @@
 // EWiseDiv (:296-298), BroadcastTo (:373-380), Summation (:400-408) and
 // Exp (:469-470).  Closed form of that chain, with P recomputed from the LSE
 // saved by the forward so no L x L tensor is ever stored:
-//   D_i  = sum_d dO_id O_id                  (pre-pass, fp32 [B,H,L])
+//   D_i  = sum_d dO_id O_id                  (row pre-pass, fp32 [B,H,L])
 //   P    = exp(s Q K^T + M - LSE)
 //   dV   = P^T dO,   dP = dO V^T,   dS = P o (dP - D)
 //   dQ   = s dS K,   dK = s dS^T Q
@@ -21,8 +21,12 @@
 //   dq:   workgroup = NW waves x 32 queries (lane = query, as the forward);
 //         loops over key tiles: S^T and dP^T from K / V row reads,
 //         dQ^T += K^T dS^T from transpose reads of the same K tile.
-// All tiles are filled by direct global->LDS loads.  Loads past the end of a
-// sequence read a clamped (valid) row and the result is masked, so the
+// bf16 at d >= 64: the dq kernel (attn_bwd_dq_pipe_kernel) runs first and
+// also writes the rows -D and LSE log2(e) the dkdv kernel reads; d = 32 runs
+// a separate row pre-pass (attn_bwd_delta_kernel), then dkdv, then dq.  fp32
+// (attn_bwd_f32.h): the pre-pass, then one launch holding both roles.
+// All bf16 tiles are filled by direct global->LDS loads.  Loads past the end
+// of a sequence read a clamped (valid) row and the result is masked, so the
 // inner loops carry no load guards.
 #include <hip/hip_runtime.h>
 
