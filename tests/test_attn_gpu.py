@@ -12,6 +12,7 @@ every head, through size-independent identities of the exact result:
   sum_j dK_j = 0               (rows of dS sum to 0)
   sum_i dQ_i . Q_i = sum_j dK_j . K_j   (both s sum_ij dS_ij q_i . k_j)
   causal: O[0] = V[0] and LSE[0] = s q_0 . k_0
+and every head of the bf16 result against the fp32 kernels on the same inputs.
 """
 import math
 import sys
@@ -140,6 +141,29 @@ def _sampled_heads(name, x, o, lse, dq, dk, dv, scale, causal, heads, tol):
         _check("dV", dv[bb, hh], rv, tol)
 
 
+def _all_heads_vs_f32(capi, name, x, o, lse, dq, dk, dv, scale, causal, tol):
+    """Every head of the bf16 result against the fp32 kernels' result on the
+    same (bf16-valued) inputs: a second, independently tiled kernel family
+    (128-query / 128-key workgroups on the fp32 MFMA, its own schedules),
+    itself held to 1e-4 against the oracle elsewhere.  Per head and tensor,
+    max|bf16 - f32| / max|f32| <= the bf16 tolerance, so a head whose rows the
+    bf16 kernels mapped, masked or scaled wrongly fails even when it is not
+    one of the sampled heads."""
+    b32 = _run_fwd(capi, x, "f32", scale, causal)
+    o32, l32 = b32["o"].download(), b32["lse"].download()
+    q32, k32, v32 = _run_bwd(capi, b32, x["do"], "f32", scale, causal)
+    worst = {}
+    for n, a, r in (("O", o, o32), ("LSE", lse, l32), ("dQ", dq, q32), ("dK", dk, k32), ("dV", dv, v32)):
+        a64, r64 = a.astype(np.float64), r.astype(np.float64)
+        ax = tuple(range(2, a64.ndim))
+        err = np.abs(a64 - r64).max(axis=ax) / np.maximum(np.abs(r64).max(axis=ax), 1e-30)
+        bb, hh = np.unravel_index(int(np.argmax(err)), err.shape)
+        worst[n] = (float(err.max()), int(bb), int(hh))
+    _say(f"  {name} every head vs fp32 kernels: " + ", ".join(f"{n} {e:.2e} at ({b},{h})" for n, (e, b, h) in worst.items()))
+    for n, (e, b, h) in worst.items():
+        assert e <= tol, f"{name} {n} head ({b},{h}): {e:.3e} > {tol:g}"
+
+
 def test_c3_bf16_causal_fwd_bwd(capi):
     cfg = orc.CONFIGS[3]
     _say("c3: bf16 causal fwd+bwd B=16 H=16 L=1024 d=64")
@@ -149,6 +173,7 @@ def test_c3_bf16_causal_fwd_bwd(capi):
     dq, dk, dv = _run_bwd(capi, b, x["do"], "bf16", cfg.scale, True)
     _sampled_heads("c3", x, o, lse, dq, dk, dv, cfg.scale, True, [(0, 0), (7, 3), (15, 15)], TOL["bf16"])
     _identities("c3", x, o, lse, dq, dk, dv, cfg.scale, True, TOL["bf16"])
+    _all_heads_vs_f32(capi, "c3", x, o, lse, dq, dk, dv, cfg.scale, True, TOL["bf16"])
 
 
 def test_c5_bf16_causal_fwd_bwd(capi):
@@ -160,6 +185,7 @@ def test_c5_bf16_causal_fwd_bwd(capi):
     dq, dk, dv = _run_bwd(capi, b, x["do"], "bf16", cfg.scale, True)
     _sampled_heads("c5", x, o, lse, dq, dk, dv, cfg.scale, True, [(0, 0), (3, 31)], TOL["bf16"])
     _identities("c5", x, o, lse, dq, dk, dv, cfg.scale, True, TOL["bf16"])
+    _all_heads_vs_f32(capi, "c5", x, o, lse, dq, dk, dv, cfg.scale, True, TOL["bf16"])
 
 
 def test_c4_bf16_decode(capi):
