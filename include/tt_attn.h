@@ -169,7 +169,11 @@ int tt_fill_normal(int dtype, void* dst, int64_t n, uint64_t seed, float scale, 
  * q [B,H,Lq,d], k/v [B,H,Lk,d], o [B,H,Lq,d], lse [B,H,Lq] (may be NULL).
  * d in {32, 64, 128}; causal requires Lq == Lk; Lk >= 1 when Lq >= 1.
  * Replaces the composition at optimizer/operators.py:163-164 (Q @ K^T),
- * :234-239 (* s), :194-196 (+ mask), :611-612 (softmax), :416-419 (@ V). */
+ * :234-239 (* s), :194-196 (+ mask), :611-612 (softmax), :416-419 (@ V).
+ * The bf16 forward allocates nothing.  The fp32 forward of a problem with
+ * fewer query tiles than the GPU has workgroup slots splits the keys and
+ * merges partial results through a per-stream library workspace (allocated
+ * on first use, TT_ERR_NOMEM if that fails). */
 int tt_attn_fwd_f32(const float* q, const float* k, const float* v, float* o, float* lse,
                     int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t d,
                     float scale, int causal, void* stream);
