@@ -145,8 +145,6 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_b
 #pragma unroll
     for (int c = 0; c < NC; ++c)
       kf[c] = __builtin_bit_cast(bf16x8, ldg16(K + kbase + (int64_t)kr * D + 16 * c + 8 * g));
-#pragma unroll
-    for (int c = KR; c < NC; ++c) *reinterpret_cast<bf16x8*>(&sKf[((c - KR) * NW + w) * 512 + 8 * l]) = kf[c];
   }
   // K operand of chunk c (each lane reads back only what it parked itself)
   uint32_t kofs = a0 + kOK + 16 * (64 * w + l);
@@ -341,8 +339,12 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_b
   for (int s0 = 0; s0 < S - 1; ++s0) issue_next();
   // Retire the K row loads (and the first tiles with them) here: otherwise
   // the compiler, which does not see the tile loads, keeps the K loads
-  // pending around the loop and waits for them on every iteration.
+  // pending around the loop and waits for them on every iteration.  The K
+  // chunks parked in LDS are stored only now, so that their wait does not
+  // hold back the tile loads above (the two HBM round trips overlap).
   wait_vmem_le<0>();
+#pragma unroll
+  for (int c = KR; c < NC; ++c) *reinterpret_cast<bf16x8*>(&sKf[((c - KR) * NW + w) * 512 + 8 * l]) = kf[c];
   const int qfull = (Lq / BQ) * BQ;
   const int qdiag = CAUSAL ? min(k0 + BN, Lq) : qstart;  // [qstart, qdiag): tiles crossing the diagonal
   run(qstart, qdiag, std::true_type{});
@@ -549,6 +551,21 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_pipe_kernel(
   const int64_t qbase = (int64_t)bh * Lq * D;
   const int64_t kbase = (int64_t)bh * Lk * D;
 
+  const int kend = CAUSAL ? min(Lk, q0 + BM) : Lk;  // >= 1
+  const int ntiles = (kend + BN - 1) / BN;
+  Dma dma;
+  dma.init();
+  int issued = 0;
+  auto issue_tile = [&](int n) {  // tile n into ring buffer n % S (n < ntiles)
+    u16* dst = smem + 2 * (n % S) * TE;
+    dma.issue(K + kbase, BN * n, Lk, dst);
+    dma.issue(V + kbase, BN * n, Lk, dst + TE);
+  };
+  // The first K / V tiles go out before the Q / dO / O row loads, so that
+  // their HBM round trip overlaps the rows' (whose wait, for the D pre-pass
+  // below, then also covers them: loads retire in issue order).
+  for (; issued < S - 1 && issued < ntiles; ++issued) issue_tile(issued);
+
   bf16x8 qf[NC], dof[NC];
   float lse2, ndl;
   {
@@ -577,8 +594,6 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_pipe_kernel(
 #pragma unroll
   for (int dt = 0; dt < ND; ++dt) adq[dt] = f32x16{};
 
-  const int kend = CAUSAL ? min(Lk, q0 + BM) : Lk;  // >= 1
-  const int ntiles = (kend + BN - 1) / BN;
   // Last block this wave computes: its diagonal block (causal) or the last
   // one.  Every earlier block lies inside Lk and before every query of the
   // wave; the last one is always computed with the mask.
@@ -600,15 +615,6 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_pipe_kernel(
       tidx[1][dt] = Tile::at4(trow + 8, 32 * dt + tcol);
     }
   }
-
-  Dma dma;
-  dma.init();
-  int issued = 0;
-  auto issue_tile = [&](int n) {  // tile n into ring buffer n % S (n < ntiles)
-    u16* dst = smem + 2 * (n % S) * TE;
-    dma.issue(K + kbase, BN * n, Lk, dst);
-    dma.issue(V + kbase, BN * n, Lk, dst + TE);
-  };
 
   // S^T and dP^T of the block in ring buffer B
   auto sdp = [&](auto b_tag, f32x16& s, f32x16& dp) __attribute__((always_inline)) {
@@ -660,8 +666,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_pipe_kernel(
     }
   };
 
-  for (; issued < S - 1 && issued < ntiles; ++issued) issue_tile(issued);
-  wait_vmem_le<0>();  // also retires the Q / dO / O / LSE loads before the loop
+  wait_vmem_le<0>();  // the first tiles, and the Q / dO / O / LSE loads, before the loop
   __syncthreads();
 
   using B0 = std::integral_constant<int, 0>;
