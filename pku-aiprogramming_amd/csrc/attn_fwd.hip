@@ -529,8 +529,8 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fwd_bf16_pipe_kernel(
 // fp32 forward.  With nsplit > 1 the key range of each query tile is split
 // over nsplit workgroups (workgroup id = split * nqt * BH + tile id), each
 // writing its unnormalised O, running max and row sum to `part`; the combine
-// kernel below merges them.  Small problems (c2: 128 query tiles) then still
-// put a workgroup on every CU.
+// kernel below merges them.  Small problems (B = H = 8, L = 256: 128 query
+// tiles) then still put a workgroup on every CU.
 template <int D, bool CAUSAL>
 __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void attn_fwd_f32_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
