@@ -104,6 +104,48 @@ def test_two_threads_one_shared_stream(capi):
         s.destroy()
 
 
+def test_two_streams_fp32_split_forward(capi):
+    """The fp32 forward of a small problem splits its keys and merges the
+    partials through a per-stream workspace: two threads, two streams,
+    different shapes, every result against the oracle (fp32 bar)."""
+    shapes = [(1, 3, 200, 64, False), (2, 2, 130, 128, True)]
+    streams = [capi.Stream(), capi.Stream()]
+    errors = []
+
+    def work(i):
+        try:
+            B, H, L, d, causal = shapes[i]
+            rng = np.random.default_rng(40 + i)
+            x = {n: rng.standard_normal((B, H, L, d), dtype=np.float32) for n in ("q", "k", "v")}
+            scale = float(np.float32(1 / math.sqrt(d)))
+            o_ref, l_ref = orc.attn_fwd_f64(x["q"], x["k"], x["v"], scale, causal)
+            b = {n: capi.DeviceBuffer.from_numpy(a, "f32") for n, a in x.items()}
+            for _ in range(4):
+                o = capi.DeviceBuffer((B, H, L, d), "f32")
+                lse = capi.DeviceBuffer((B, H, L), "f32")
+                capi.attn_fwd(b["q"], b["k"], b["v"], o, lse, scale, causal, stream=streams[i].handle)
+                capi.lib().call("tt_stream_sync", streams[i].handle)
+                for n, a, r in (("O", o.download(), o_ref), ("LSE", lse.download(), l_ref)):
+                    e = orc.max_rel_err(a, r)
+                    if e > orc.TOL["f32"]:
+                        errors.append(f"thread {i} {n}: {e:.3e}")
+        except Exception as exc:  # surfaced below
+            errors.append(f"thread {i}: {exc!r}")
+
+    _say("two threads, two streams: fp32 split forward [1,3,200,64] and causal [2,2,130,128], 4 reps each")
+    try:
+        th = [threading.Thread(target=work, args=(i,)) for i in range(2)]
+        for t in th:
+            t.start()
+        for t in th:
+            t.join(timeout=120)
+        assert not any(t.is_alive() for t in th), "a worker thread did not finish"
+        assert not errors, errors
+    finally:
+        for st in streams:
+            st.destroy()
+
+
 def test_library_stream_cannot_be_destroyed(capi):
     L = capi.lib()
     rc = L.lib.tt_stream_destroy(L.lib.tt_stream())
