@@ -1,6 +1,10 @@
 // fp32 attention backward kernels (dK/dV and dQ) on v_mfma_f32_32x32x2f32,
 // included by attn_bwd.hip.  Each fp32 MFMA takes one k-value per lane half,
 // so the transposed operands are plain column reads of row-major LDS tiles.
+// In the contractions over d, MFMA step c takes d-index c in lane half 0 and
+// D/2 + c in lane half 1: a lane's row operands are D/2 consecutive floats
+// (16-byte global loads), and the two lane halves read disjoint banks of the
+// odd-pitch LDS tiles.
 #pragma once
 
 #include "attn_common.h"
@@ -50,10 +54,13 @@ __device__ __forceinline__ void bwd_f32_dkdv(int id, float* smem, const float* _
   float kf[NC], vf[NC];
   {
     const int kr = min(key, Lk - 1);
+    const int64_t at = kbase + (int64_t)kr * D + g * (D / 2);
 #pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      kf[c] = K[kbase + (int64_t)kr * D + 2 * c + g];
-      vf[c] = V[kbase + (int64_t)kr * D + 2 * c + g];
+    for (int c4 = 0; c4 < NC / 4; ++c4) {
+      const float4 kx = *reinterpret_cast<const float4*>(K + at + 4 * c4);
+      const float4 vx = *reinterpret_cast<const float4*>(V + at + 4 * c4);
+      kf[4 * c4] = kx.x, kf[4 * c4 + 1] = kx.y, kf[4 * c4 + 2] = kx.z, kf[4 * c4 + 3] = kx.w;
+      vf[4 * c4] = vx.x, vf[4 * c4 + 1] = vx.y, vf[4 * c4 + 2] = vx.z, vf[4 * c4 + 3] = vx.w;
     }
   }
   f32x16 adk[ND], adv[ND];
@@ -105,8 +112,8 @@ __device__ __forceinline__ void bwd_f32_dkdv(int id, float* smem, const float* _
       f32x16 s = f32x16{}, dp = f32x16{};
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
-        s = mfma_f32_32x32x2(sQ[(32 * mt + r32) * P + 2 * c + g], kf[c], s);
-        dp = mfma_f32_32x32x2(sdO[(32 * mt + r32) * P + 2 * c + g], vf[c], dp);
+        s = mfma_f32_32x32x2(sQ[(32 * mt + r32) * P + g * (D / 2) + c], kf[c], s);
+        dp = mfma_f32_32x32x2(sdO[(32 * mt + r32) * P + g * (D / 2) + c], vf[c], dp);
       }
       const bool need_mask = CAUSAL && (qb + 32 * mt < wk_lo + 31);
       float pr[16], dsr[16];
@@ -171,10 +178,13 @@ __device__ __forceinline__ void bwd_f32_dq(int id, float* smem, const float* __r
   float qf[NC], dof[NC];
   {
     const int qr = min(qrow, Lq - 1);
+    const int64_t at = qbase + (int64_t)qr * D + g * (D / 2);
 #pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      qf[c] = Q[qbase + (int64_t)qr * D + 2 * c + g];
-      dof[c] = dO[qbase + (int64_t)qr * D + 2 * c + g];
+    for (int c4 = 0; c4 < NC / 4; ++c4) {
+      const float4 qx = *reinterpret_cast<const float4*>(Q + at + 4 * c4);
+      const float4 ox = *reinterpret_cast<const float4*>(dO + at + 4 * c4);
+      qf[4 * c4] = qx.x, qf[4 * c4 + 1] = qx.y, qf[4 * c4 + 2] = qx.z, qf[4 * c4 + 3] = qx.w;
+      dof[4 * c4] = ox.x, dof[4 * c4 + 1] = ox.y, dof[4 * c4 + 2] = ox.z, dof[4 * c4 + 3] = ox.w;
     }
   }
   const float lse2 = qrow < Lq ? LSE[(int64_t)bh * Lq + qrow] * kLog2e : INFINITY;
@@ -219,8 +229,8 @@ __device__ __forceinline__ void bwd_f32_dq(int id, float* smem, const float* __r
       f32x16 s = f32x16{}, dp = f32x16{};
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
-        s = mfma_f32_32x32x2(sK[(32 * t + r32) * P + 2 * c + g], qf[c], s);
-        dp = mfma_f32_32x32x2(sV[(32 * t + r32) * P + 2 * c + g], dof[c], dp);
+        s = mfma_f32_32x32x2(sK[(32 * t + r32) * P + g * (D / 2) + c], qf[c], s);
+        dp = mfma_f32_32x32x2(sV[(32 * t + r32) * P + g * (D / 2) + c], dof[c], dp);
       }
       float dsr[16];
 #pragma unroll

@@ -541,11 +541,12 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void attn_fwd_f32_kernel(
   constexpr int ND = D / 32;
   constexpr int CPR = D / 4;  // 16-byte chunks per row
   constexpr int LPT = BN * CPR / 256;
-  // K rows with d-index k at column (k & 1) * D/2 + k/2, so that the k-values
-  // 2c + g of consecutive MFMAs are adjacent for lane half g (one 16-byte read
-  // feeds four MFMAs); V stored transposed, sV[d][key], so that the four keys
-  // of four consecutive accumulator rows are adjacent.  Row pitches of 4 mod
-  // 64 floats put the 16 rows of a 16-lane read pass on distinct banks.
+  // MFMA step c contracts d-indices c (lane half 0) and D/2 + c (lane half 1):
+  // a lane's Q values and K operands are then D/2 consecutive floats, read
+  // 16 bytes at a time (one K read feeds four MFMAs).  V is stored
+  // transposed, sV[d][key], so that the four keys of four consecutive
+  // accumulator rows are adjacent.  Row pitches of 4 mod 64 floats put the 16
+  // rows of a 16-lane read pass on distinct banks.
   constexpr int PK = D + 4, PV = BN + 4;
   __shared__ __align__(16) float sK[BN * PK];
   __shared__ __align__(16) float sV[D * PV];
@@ -563,8 +564,15 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void attn_fwd_f32_kernel(
   float qf[NC];
   {
     const int qr = min(qrow, Lq - 1);
+    const float* qp = Q + qbase + (int64_t)qr * D + g * (D / 2);
 #pragma unroll
-    for (int c = 0; c < NC; ++c) qf[c] = Q[qbase + (int64_t)qr * D + 2 * c + g];
+    for (int c4 = 0; c4 < NC / 4; ++c4) {
+      const float4 x = *reinterpret_cast<const float4*>(qp + 4 * c4);
+      qf[4 * c4] = x.x;
+      qf[4 * c4 + 1] = x.y;
+      qf[4 * c4 + 2] = x.z;
+      qf[4 * c4 + 3] = x.w;
+    }
   }
 
   f32x16 acc[ND];
@@ -593,9 +601,7 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void attn_fwd_f32_kernel(
     for (int i = 0; i < LPT; ++i) {
       const int c = tid + 256 * i;
       const int key = c / CPR, ch = c % CPR;  // d-indices 4ch .. 4ch + 3
-      float* pk = &sK[key * PK + 2 * ch];
-      *reinterpret_cast<float2*>(pk) = float2{kreg[i].x, kreg[i].z};          // even k
-      *reinterpret_cast<float2*>(pk + D / 2) = float2{kreg[i].y, kreg[i].w};  // odd k
+      *reinterpret_cast<float4*>(&sK[key * PK + 4 * ch]) = kreg[i];
       float* pv = &sV[4 * ch * PV + key];
       pv[0] = vreg[i].x;
       pv[PV] = vreg[i].y;
