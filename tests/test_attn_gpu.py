@@ -368,6 +368,33 @@ def test_decode_shapes(capi, dtype, Lkv, d):
     _check("lse", bl.download(), l_ref[..., 0], tol)
 
 
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_repeated_calls_are_bitwise_identical(capi, dtype):
+    """No atomics and a fixed reduction order: the same inputs give the same
+    bits on every call (forward, backward and decode), including the fp32
+    forward's key split and combine."""
+    B, H, L, d = 2, 3, 300, 64
+    _say(f"determinism {dtype} [{B},{H},{L},{d}] causal fwd+bwd, decode, 3 calls")
+    rng = np.random.default_rng(77)
+    x = {n: rng.standard_normal((B, H, L, d), dtype=np.float32) for n in ("q", "k", "v", "do")}
+    scale = float(np.float32(1 / math.sqrt(d)))
+    runs = []
+    for _ in range(3):
+        b = _run_fwd(capi, x, dtype, scale, True)
+        ddo = capi.DeviceBuffer.from_numpy(x["do"], dtype)
+        g = [capi.DeviceBuffer((B, H, L, d), dtype) for _ in range(3)]
+        capi.attn_bwd(b["q"], b["k"], b["v"], b["o"], b["lse"], ddo, *g, scale, True)
+        q1 = capi.DeviceBuffer.from_numpy(x["q"][:, :, :1].copy(), dtype)
+        o1 = capi.DeviceBuffer((B, H, 1, d), dtype)
+        l1 = capi.DeviceBuffer((B, H), "f32")
+        capi.attn_decode(q1, b["k"], b["v"], o1, l1, scale)
+        capi.lib().sync()
+        runs.append([t.download_bytes() for t in (b["o"], b["lse"], *g, o1, l1)])
+    for later in runs[1:]:
+        for name, a, r in zip(("O", "LSE", "dQ", "dK", "dV", "decode o", "decode lse"), later, runs[0]):
+            assert np.array_equal(a.view(np.uint8), r.view(np.uint8)), f"{name} differs between calls"
+
+
 def test_empty_inputs_are_noops(capi):
     z = capi.DeviceBuffer((0, 2, 16, 64), "bf16")
     capi.attn_fwd(z, z, z, z, None, 0.125, True)
