@@ -117,7 +117,9 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_b
   // global->LDS loads, then the parked K chunks (lane-linear: chunk KR + c of
   // lane l of wave w at 16 (64 (c NW + w) + l) bytes).
   constexpr int kOQ = 0, kOdO = kOQ + 2 * S * TE, kOV = kOdO + 2 * S * TE, kOL = kOV + 2 * Tile::kElems(BN),
-                kOD = kOL + 4 * S * VS, kOK = kOD + 4 * S * VS, kLds = kOK + (KL > 0 ? KL : 1) * NW * 1024;
+                kOD = kOL + 4 * S * VS, kOK = kOD + 4 * S * VS, kLds = kOK + (KL > 0 ? KL * NW * 1024 : 16);
+  // (no parked K at d <= 64: 50 KB then lets three workgroups share a CU at
+  // d = 64, which a 54 KB block did not; the dK/dV kernel ran 8 % faster)
   static_assert(kOV <= 65536, "Q / dO ring offsets exceed the 16-bit LDS immediate");
   __shared__ __align__(16) char smem[kLds];
   u16* const sQ = reinterpret_cast<u16*>(smem + kOQ);
