@@ -76,7 +76,12 @@ int tt_stream_destroy(void* stream);
  * with TT_FAIL_ALLOC_AFTER=n in the environment, the process's device
  * allocations n, n+1, ... are refused (failure injection for tests). */
 int tt_malloc(void** ptr, size_t bytes);
-/* Replaces cudaFree at src/Tinytensor.cu:90,108,239,378.  NULL is a no-op. */
+/* Replaces cudaFree at src/Tinytensor.cu:90,108,239,378.  NULL is a no-op.
+ * Unlike cudaFree it does not wait for the device: the block goes back to
+ * the cache at once, and its next owner's work is ordered after the freed
+ * block's last use only when both run on the library stream.  Work queued
+ * on a caller stream that still reads or writes the block must have
+ * finished (tt_stream_sync) before the block is freed. */
 int tt_free(void* ptr);
 int tt_empty_cache(void);
 /* Bytes currently handed out / held in the cache. */

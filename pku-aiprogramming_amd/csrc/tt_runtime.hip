@@ -6,6 +6,7 @@
 // work is ordered on one library stream; host-visible copies wait for it.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -38,12 +39,14 @@ int hip_fail(hipError_t e, const char* what) {
 }
 
 static std::mutex g_mu;
-static bool g_inited = false;
+// Set (release) by tt_init after the device, stream and scratch address are
+// in place; read (acquire) without the lock on every call.
+static std::atomic<bool> g_inited{false};
 static int g_device = 0;
 static hipStream_t g_stream = nullptr;
 
 int ensure_init() {
-  if (g_inited) return TT_OK;
+  if (g_inited.load(std::memory_order_acquire)) return TT_OK;
   return tt_init(g_device);
 }
 
@@ -81,12 +84,19 @@ static BlockCache<HipBackend> g_blocks(g_backend);
 static WorkspaceCache<HipBackend> g_ws(g_backend, g_blocks);
 
 // ---------------------------------------------------------------- instrumentation
+// Events to record after the next launches (tt_set_launch_events).  The
+// count is read without the lock, so launches pay nothing while none is set.
+static std::mutex g_ev_mu;
 static std::vector<void*> g_launch_events;
 static size_t g_launch_next = 0;
+static std::atomic<size_t> g_launch_left{0};
 
 void after_launch(hipStream_t s) {
+  if (g_launch_left.load(std::memory_order_acquire) == 0) return;
+  std::lock_guard<std::mutex> lk(g_ev_mu);
   if (g_launch_next >= g_launch_events.size()) return;
   (void)hipEventRecord((hipEvent_t)g_launch_events[g_launch_next++], s);
+  g_launch_left.store(g_launch_events.size() - g_launch_next, std::memory_order_release);
 }
 
 // ---------------------------------------------------------------- allocation-free scratch
@@ -100,7 +110,7 @@ static void* g_scratch_ptr[kMaxDevices] = {};
 
 void* noalloc_scratch(size_t* bytes) {
   if (bytes) *bytes = kNoAllocScratchBytes;
-  if (!g_inited) return nullptr;
+  if (!g_inited.load(std::memory_order_acquire)) return nullptr;
   return g_scratch_ptr[g_device];
 }
 
@@ -265,7 +275,7 @@ int tt_init(int device) {
   // Default priority on purpose: one stream, ordinary priority.
   TT_HIP(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
   g_device = device;
-  g_inited = true;
+  g_inited.store(true, std::memory_order_release);
   return ok();
 }
 
@@ -321,7 +331,7 @@ int tt_free(void* ptr) {
 }
 
 int tt_empty_cache(void) {
-  if (!g_inited) return TT_OK;
+  if (!g_inited.load(std::memory_order_acquire)) return TT_OK;
   TT_HIP(hipStreamSynchronize(g_stream));
   const int rc = g_ws.release_all();
   g_blocks.trim();
@@ -387,9 +397,11 @@ int tt_event_destroy(void* ev) {
 }
 
 int tt_set_launch_events(void** evs, int n) {
+  std::lock_guard<std::mutex> lk(g_ev_mu);
   g_launch_events.clear();
   g_launch_next = 0;
   if (evs && n > 0) g_launch_events.assign(evs, evs + n);
+  g_launch_left.store(g_launch_events.size(), std::memory_order_release);
   return TT_OK;
 }
 
