@@ -78,6 +78,24 @@ def decode_bytes(B, H, Lkv, d):
     return 2 * (B * H * Lkv * d * 2) + 2 * (B * H * d * 2)
 
 
+# Untimed run-in before every GPU measurement.  The GPU lowers its clock while
+# it idles (between workloads, while a CPU baseline runs) and needs tens of
+# milliseconds of load to come back to the steady clock it holds at the
+# board's power limit; a few warm-up steps of a short workload end inside that
+# ramp (c3 measured 0.25-0.27 ms per step right after idle against 0.214 ms
+# steady).  So each workload first runs for PREWARM_S seconds, then its
+# `warmup` steps, then the timed steps.
+PREWARM_S = 0.3
+
+
+def prewarm(T, step, seconds=PREWARM_S):
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(10):
+            step()
+        T.lib().sync()
+
+
 def run_fwdbwd(T, steps, warmup):
     B, H, L, d = C5["B"], C5["H"], C5["L"], C5["d"]
     scale = float(__import__("numpy").float32(1.0 / math.sqrt(d)))
@@ -92,6 +110,7 @@ def run_fwdbwd(T, steps, warmup):
         T.attn_fwd(q, k, v, o, lse, scale, True)
         T.attn_bwd(q, k, v, o, lse, do, dq, dk, dv, scale, True)
 
+    prewarm(T, step)
     for _ in range(warmup):
         step()
     T.lib().sync()
@@ -130,6 +149,7 @@ def run_decode(T, steps, warmup):
     v.fill_normal(4002)
     o = T.DeviceBuffer((B, H, 1, d), "bf16")
     lse = T.DeviceBuffer((B, H), "f32")
+    prewarm(T, lambda: T.attn_decode(q, k, v, o, lse, scale))
     for _ in range(warmup):
         T.attn_decode(q, k, v, o, lse, scale)
     T.lib().sync()
@@ -197,6 +217,7 @@ def run_config(T, cfg, steps, warmup):
         if cfg.backward:
             T.attn_bwd(q, k, v, o, lse, do_, *g, cfg.scale, cfg.causal)
 
+    prewarm(T, step)
     for _ in range(warmup):
         step()
     T.lib().sync()
@@ -285,6 +306,7 @@ def run_copy(T, steps, warmup, nbytes=1 << 30):
     def once():
         L.call("tt_elementwise", 4, 0, c.ptr, a.ptr, None, n, 1.0, 0.0, 0, None)  # TT_EW_SCALE, TT_F32
 
+    prewarm(T, once)
     for _ in range(warmup):
         once()
     start, stop = T.Event(), T.Event()
@@ -311,6 +333,7 @@ def run_softmax(T, steps, warmup, rows, cols):
     x = T.DeviceBuffer((rows, cols), "f32")
     y = T.DeviceBuffer((rows, cols), "f32")
     x.fill_normal(5000, 3.0)
+    prewarm(T, lambda: T.softmax_rows(x, y))
     for _ in range(warmup):
         T.softmax_rows(x, y)
     T.lib().sync()
@@ -339,6 +362,7 @@ def run_gemm(T, steps, warmup, dtype, m, n, k, ta, tb):
     Cb = T.DeviceBuffer((m, n), dtype)
     A.fill_normal(6000)
     B.fill_normal(6001)
+    prewarm(T, lambda: T.gemm(ta, tb, m, n, k, 1.0, A, B, 0.0, Cb))
     for _ in range(warmup):
         T.gemm(ta, tb, m, n, k, 1.0, A, B, 0.0, Cb)
     T.lib().sync()
@@ -567,7 +591,7 @@ def main(argv=None):
     out = {
         "metric": "attn fwd+bwd TFLOP/s (% bf16 MFMA peak); decode KV-read HBM GB/s (% peak)",
         "value": None, "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": None, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "prewarm_s": PREWARM_S, "ms_per_step": None, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "bf16", "data": "synthetic (on-device seeded N(0,1), bf16)",
         "config": {"workload": "causal attention fwd+bwd, B=4 H=32 L=4096 d=128, bf16 in / fp32 accumulate",
                    "B": C5["B"], "H": C5["H"], "L": C5["L"], "d": C5["d"], "causal": True,
