@@ -196,12 +196,30 @@ def run_decode(T, steps, warmup):
 PEAK_FP32_MFMA_TFLOPS = 157.3
 
 
+class GpuConfig:
+    """Shape of a BASELINE.json configuration as the GPU legs time it."""
+
+    def __init__(self, cid, B, H, Lq, Lk, d, dtype, causal, backward, qkv_scale=1.0):
+        self.cid, self.B, self.H, self.Lq, self.Lk, self.d = cid, B, H, Lq, Lk, d
+        self.dtype, self.causal, self.backward, self.qkv_scale = dtype, causal, backward, qkv_scale
+        self.scale = float(__import__("numpy").float32(1.0 / math.sqrt(d)))
+
+
+GPU_CONFIGS = {
+    1: GpuConfig(1, 1, 1, 64, 64, 32, "f32", False, False),
+    2: GpuConfig(2, 8, 8, 256, 256, 64, "f32", False, True),
+    3: GpuConfig(3, 16, 16, 1024, 1024, 64, "bf16", True, True, 0.5),
+    5: GpuConfig(5, C5["B"], C5["H"], C5["L"], C5["L"], C5["d"], "bf16", True, True),
+}
+
+
 def config_flops(cfg):
     f = (12.0 if cfg.backward else 4.0) * cfg.B * cfg.H * cfg.Lq * cfg.Lk * cfg.d
     return f / 2 if cfg.causal else f
 
 
-def run_config(T, cfg, steps, warmup):
+def config_buffers(T, cfg):
+    """Device inputs (seeded on the device), output and gradient buffers of `cfg`."""
     dt = cfg.dtype
     qs, ks = (cfg.B, cfg.H, cfg.Lq, cfg.d), (cfg.B, cfg.H, cfg.Lk, cfg.d)
     q, do_ = T.DeviceBuffer(qs, dt), T.DeviceBuffer(qs, dt)
@@ -211,12 +229,24 @@ def run_config(T, cfg, steps, warmup):
     o = T.DeviceBuffer(qs, dt)
     lse = T.DeviceBuffer(qs[:3], "f32")
     g = [T.DeviceBuffer(qs, dt), T.DeviceBuffer(ks, dt), T.DeviceBuffer(ks, dt)]
+    return q, k, v, do_, o, lse, g
+
+
+def config_step(T, cfg, bufs, part="all"):
+    """One step of `cfg`: forward (+ backward); part "fwd" / "bwd" runs one half."""
+    q, k, v, do_, o, lse, g = bufs
 
     def step():
-        T.attn_fwd(q, k, v, o, lse, cfg.scale, cfg.causal)
-        if cfg.backward:
+        if part in ("all", "fwd"):
+            T.attn_fwd(q, k, v, o, lse, cfg.scale, cfg.causal)
+        if cfg.backward and part in ("all", "bwd"):
             T.attn_bwd(q, k, v, o, lse, do_, *g, cfg.scale, cfg.causal)
 
+    return step
+
+
+def run_config(T, cfg, steps, warmup):
+    step = config_step(T, cfg, config_buffers(T, cfg))
     prewarm(T, step)
     for _ in range(warmup):
         step()
@@ -230,15 +260,42 @@ def run_config(T, cfg, steps, warmup):
     return T.Event.elapsed(a, b) / steps
 
 
+def run_sustain(T, cfg, part, seconds, batch=200):
+    """The step of `cfg` (part "all", "fwd" or "bwd") in batches of `batch`
+    steps for `seconds`, each batch timed with HIP events: how the rate
+    settles while the board runs at its power limit (sample the board's power
+    and clock with amd-smi meanwhile)."""
+    bufs = config_buffers(T, cfg)
+    if part == "bwd":
+        config_step(T, cfg, bufs, "fwd")()  # O and LSE for the backward
+    step = config_step(T, cfg, bufs, part)
+    for _ in range(5):
+        step()
+    T.lib().sync()
+    ms = []
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        a, b = T.Event(), T.Event()
+        a.record()
+        for _ in range(batch):
+            step()
+        b.record()
+        T.lib().sync()
+        ms.append(T.Event.elapsed(a, b) / batch)
+    return {"batches": len(ms), "batch_steps": batch, "ms_first_batch": ms[0], "ms_last_batch": ms[-1],
+            "ms_median_batch": sorted(ms)[len(ms) // 2], "ms_min_batch": min(ms)}
+
+
 def config_cpu_baseline(cfg, max_heads, reps=3):
     """The reference's op chain (oracle composition_*_f32, float32 numpy, full
     L x L materialised) on up to `max_heads` heads of the config; returns the
     rate in TFLOP/s of the same algorithmic FLOP count."""
     import numpy as np
 
+    sys.path.insert(0, ROOT)
     from oracle import attn_oracle as orc
 
-    x = orc.seeded_inputs(cfg)
+    x = orc.seeded_inputs(orc.CONFIGS[cfg.cid])
     heads = [(b, h) for b in range(cfg.B) for h in range(cfg.H)][:max_heads]
 
     def once():
@@ -562,10 +619,14 @@ def main(argv=None):
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", choices=["all", "fwdbwd", "configs", "decode", "copy", "ceiling", "softmax", "gemm", "io"],
+    ap.add_argument("--only", choices=["all", "fwdbwd", "configs", "decode", "copy", "ceiling", "softmax", "gemm", "io",
+                                       "sustain"],
                     default="all",
                     help="run one workload only (for profiler runs; 'copy' is the 1 GiB calibration copy, "
-                         "'ceiling' the library bf16 GEMM reference)")
+                         "'ceiling' the library bf16 GEMM reference, 'sustain' the --sustain loop)")
+    ap.add_argument("--sustain", default="3:all:8", metavar="CID:PART:SECONDS",
+                    help="with --only sustain: config (1, 2, 3 or 5), part (all, fwd or bwd) and duration of a "
+                         "loop of 200-step batches")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-heads", type=int, default=128)
     args = ap.parse_args(argv)
@@ -587,6 +648,15 @@ def main(argv=None):
     if T.lib().device_count() < 1:
         print("bench.py: no HIP device visible", file=sys.stderr)
         return 1
+
+    if args.only == "sustain":
+        cid, part, secs = args.sustain.split(":")
+        cfg = GPU_CONFIGS[int(cid)]
+        if part not in ("all", "fwd", "bwd"):
+            ap.error("--sustain part must be all, fwd or bwd")
+        print(json.dumps({"metric": "ms per step over a sustained loop", "config": f"c{cid}", "part": part,
+                          **run_sustain(T, cfg, part, float(secs))}), flush=True)
+        return 0
 
     out = {
         "metric": "attn fwd+bwd TFLOP/s (% bf16 MFMA peak); decode KV-read HBM GB/s (% peak)",
@@ -651,12 +721,9 @@ def main(argv=None):
             out["roofline"] = out["decode"]["roofline"]
 
     if args.only in ("all", "configs"):
-        sys.path.insert(0, ROOT)
-        from oracle import attn_oracle as orc
-
         lines = []
         for cid in (1, 2, 3):
-            cfg = orc.CONFIGS[cid]
+            cfg = GPU_CONFIGS[cid]
             ms = run_config(T, cfg, max(args.steps, 20), args.warmup)
             tf = config_flops(cfg) / (ms * 1e-3) / 1e12
             peak = PEAK_BF16_TFLOPS if cfg.dtype == "bf16" else PEAK_FP32_MFMA_TFLOPS
