@@ -1,9 +1,11 @@
 // Attention and softmax layer functions: shape checks, output sizing, then one C-ABI call.
 #include "layers.h"
 
+#include <initializer_list>
 #include <stdexcept>
 #include <string>
 #include <type_traits>
+#include <utility>
 
 namespace {
 
@@ -37,6 +39,23 @@ void check_qkv(const std::string& fn, const TinyTensor<T>& q, const TinyTensor<T
     throw std::invalid_argument(fn + ": k and v must have the same shape");
 }
 
+// Outputs must not share storage with an input or with each other: the
+// kernels read the inputs while they write the outputs, and an output's
+// resize may free the storage it held.  (Distinct tensors never share
+// storage: copies are deep, so equal data pointers mean the same tensor.)
+using Named = std::pair<const void*, const char*>;
+void no_alias(const std::string& fn, std::initializer_list<Named> inputs, std::initializer_list<Named> outputs) {
+  for (auto o = outputs.begin(); o != outputs.end(); ++o) {
+    if (!o->first) continue;
+    for (const Named& i : inputs)
+      if (i.first == o->first)
+        throw std::invalid_argument(fn + ": output " + o->second + " is the same tensor as input " + i.second);
+    for (auto o2 = outputs.begin(); o2 != o; ++o2)
+      if (o2->first == o->first)
+        throw std::invalid_argument(fn + ": outputs " + o2->second + " and " + o->second + " are the same tensor");
+  }
+}
+
 }  // namespace
 
 template <typename T>
@@ -47,6 +66,7 @@ void AttentionForward(const TinyTensor<T>& q, const TinyTensor<T>& k, const Tiny
   check_qkv(fn, q, k, v, dq, dk);
   need_gpu(fn, "out", out.device);
   need_gpu(fn, "lse", lse.device);
+  no_alias(fn, {{q.p_data, "q"}, {k.p_data, "k"}, {v.p_data, "v"}}, {{out.p_data, "out"}, {lse.p_data, "lse"}});
   out.resize(q.shape);
   lse.resize(std::vector<int>{dq.B, dq.H, dq.L});
   int rc;
@@ -79,6 +99,10 @@ void AttentionBackward(const TinyTensor<T>& q, const TinyTensor<T>& k, const Tin
   if (grad_out.shape != q.shape) throw std::invalid_argument(fn + ": grad_out must have the shape of q");
   if (lse.shape != std::vector<int>{dq.B, dq.H, dq.L})
     throw std::invalid_argument(fn + ": lse must have shape [B, H, Lq]");
+  no_alias(fn,
+           {{q.p_data, "q"}, {k.p_data, "k"}, {v.p_data, "v"}, {out.p_data, "out"}, {lse.p_data, "lse"},
+            {grad_out.p_data, "grad_out"}},
+           {{grad_q.p_data, "grad_q"}, {grad_k.p_data, "grad_k"}, {grad_v.p_data, "grad_v"}});
   grad_q.resize(q.shape);
   grad_k.resize(k.shape);
   grad_v.resize(v.shape);
@@ -106,6 +130,7 @@ void AttentionDecode(const TinyTensor<T>& q, const TinyTensor<T>& k_cache, const
   check_qkv(fn, q, k_cache, v_cache, dq, dk);
   need_gpu(fn, "out", out.device);
   if (dq.L != 1) throw std::invalid_argument(fn + ": q must have Lq == 1");
+  no_alias(fn, {{q.p_data, "q"}, {k_cache.p_data, "k_cache"}, {v_cache.p_data, "v_cache"}}, {{out.p_data, "out"}});
   out.resize(q.shape);
   int rc;
   if constexpr (std::is_same<T, float>::value)

@@ -158,6 +158,35 @@ def test_layer_rejects_bad_shapes(mods):
         ml.AttentionForward(q3, q3, q3, out, lse, 0.1, False)
 
 
+@pytest.mark.parametrize("dtype", ["float32", "bf16"])
+def test_layer_rejects_outputs_aliasing_inputs(mods, dtype):
+    """An output that is one of the inputs (or another output) is refused
+    before any resize or launch, and the inputs keep their data."""
+    mt, ml = mods
+    T = _cls(mt, dtype)
+    rng = np.random.default_rng(7)
+    x = {n: orc.bf16_round(rng.standard_normal((1, 2, 64, 32), dtype=np.float32)) for n in ("q", "k", "v", "do")}
+    q, k, v, do = (T(x[n], "gpu") for n in ("q", "k", "v", "do"))
+    kl = T(orc.bf16_round(rng.standard_normal((1, 2, 96, 32), dtype=np.float32)), "gpu")
+    out, lse = T([1], "gpu"), mt.Tensor_float([1], "gpu")
+    with pytest.raises(ValueError, match="out is the same tensor as input q"):
+        ml.AttentionForward(q, k, v, q, lse, 0.1, False)
+    with pytest.raises(ValueError, match="out is the same tensor as input k"):
+        ml.AttentionForward(q, kl, kl, kl, lse, 0.1, False)  # its resize would free k
+    ml.AttentionForward(q, k, v, out, lse, 0.1, True)
+    gq, gk = T([1], "gpu"), T([1], "gpu")
+    with pytest.raises(ValueError, match="grad_v is the same tensor as input v"):
+        ml.AttentionBackward(q, k, v, out, lse, do, gq, gk, v, 0.1, True)
+    with pytest.raises(ValueError, match="outputs grad_q and grad_k are the same tensor"):
+        ml.AttentionBackward(q, k, v, out, lse, do, gq, gq, gk, 0.1, True)
+    q1 = T(x["q"][:, :, :1], "gpu")
+    with pytest.raises(ValueError, match="out is the same tensor as input q"):
+        ml.AttentionDecode(q1, k, v, q1, 0.1)
+    for n, t in (("q", q), ("k", k), ("v", v), ("do", do)):
+        np.testing.assert_array_equal(np.asarray(t.numpy(), np.float32).reshape(x[n].shape), x[n], err_msg=n)
+    assert kl.numpy().shape == (1, 2, 96, 32)
+
+
 # ------------------------------------------------------------------ autograd operator
 
 @pytest.fixture(scope="module")
