@@ -824,6 +824,12 @@ static int bwd_prologue(const char* fn, const T* q, const T* k, const T* v, cons
   }
   if (!q || !k || !v || !o || !lse || !dout || !dq || !dk || !dv)
     return fail(TT_ERR_ARG, std::string(fn) + ": null pointer");
+  const size_t qb = (size_t)(BH * Lq * d) * sizeof(T), kb = (size_t)(BH * Lk * d) * sizeof(T);
+  if ((rc = check_no_overlap(fn,
+                             {{q, qb, "q"}, {k, kb, "k"}, {v, kb, "v"}, {o, qb, "o"},
+                              {lse, (size_t)(BH * Lq) * sizeof(float), "lse"}, {dout, qb, "dO"}},
+                             {{dq, qb, "dQ"}, {dk, kb, "dK"}, {dv, kb, "dV"}})))
+    return rc;
   *done = false;
   return TT_OK;
 }

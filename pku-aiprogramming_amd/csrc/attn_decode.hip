@@ -220,6 +220,10 @@ static int decode_entry(const char* fn, const T* q, const T* k, const T* v, T* o
   const int64_t BH = B * H;
   if (BH == 0) return ok();
   if (!q || !k || !v || !o) return fail(TT_ERR_ARG, std::string(fn) + ": null pointer");
+  const size_t qb = (size_t)(BH * d) * sizeof(T), kb = (size_t)(BH * Lkv * d) * sizeof(T);
+  if ((rc = check_no_overlap(fn, {{q, qb, "q"}, {k, kb, "k"}, {v, kb, "v"}},
+                             {{o, qb, "o"}, {lse, (size_t)BH * sizeof(float), "lse"}})))
+    return rc;
   if ((rc = ensure_init())) return rc;
   hipStream_t st = stream_or_default(stream);
   switch (d) {

@@ -828,6 +828,12 @@ extern "C" int tt_attn_fwd_f32(const float* q, const float* k, const float* v, f
   const int64_t BH = B * H;
   if (BH == 0 || Lq == 0) return ok();
   if (!q || !k || !v || !o) return fail(TT_ERR_ARG, "tt_attn_fwd_f32: null pointer");
+  {
+    const size_t qb = (size_t)(BH * Lq * d) * sizeof(float), kb = (size_t)(BH * Lk * d) * sizeof(float);
+    if ((rc = check_no_overlap("tt_attn_fwd_f32", {{q, qb, "q"}, {k, kb, "k"}, {v, kb, "v"}},
+                               {{o, qb, "o"}, {lse, (size_t)(BH * Lq) * sizeof(float), "lse"}})))
+      return rc;
+  }
   if ((rc = ensure_init())) return rc;
   hipStream_t st = stream_or_default(stream);
   TT_FWD_DISPATCH(fwd_f32)
@@ -841,6 +847,12 @@ extern "C" int tt_attn_fwd_bf16(const uint16_t* q, const uint16_t* k, const uint
   const int64_t BH = B * H;
   if (BH == 0 || Lq == 0) return ok();
   if (!q || !k || !v || !o) return fail(TT_ERR_ARG, "tt_attn_fwd_bf16: null pointer");
+  {
+    const size_t qb = (size_t)(BH * Lq * d) * sizeof(uint16_t), kb = (size_t)(BH * Lk * d) * sizeof(uint16_t);
+    if ((rc = check_no_overlap("tt_attn_fwd_bf16", {{q, qb, "q"}, {k, kb, "k"}, {v, kb, "v"}},
+                               {{o, qb, "o"}, {lse, (size_t)(BH * Lq) * sizeof(float), "lse"}})))
+      return rc;
+  }
   if ((rc = ensure_init())) return rc;
   hipStream_t st = stream_or_default(stream);
   TT_FWD_DISPATCH(fwd_bf16)

@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <initializer_list>
 #include <string>
 
 #include "tt_internal.h"
@@ -57,6 +58,33 @@ inline int check_attn_shape(const char* fn, int64_t B, int64_t H, int64_t Lq, in
   if (Lq > 0 && Lk == 0 && B * H > 0) return fail(TT_ERR_ARG, f + ": softmax over zero keys");
   if (Lq > (int64_t(1) << 30) || Lk > (int64_t(1) << 30)) return fail(TT_ERR_ARG, f + ": sequence too long");
   if (B * H > (int64_t(1) << 24)) return fail(TT_ERR_ARG, f + ": too many heads");
+  return TT_OK;
+}
+
+// Byte range of one launcher argument, for the overlap check below.
+struct ArgSpan {
+  const void* p;
+  size_t bytes;
+  const char* name;
+};
+inline bool spans_overlap(const ArgSpan& a, const ArgSpan& b) {
+  if (!a.p || !b.p || a.bytes == 0 || b.bytes == 0) return false;
+  const uintptr_t a0 = (uintptr_t)a.p, b0 = (uintptr_t)b.p;
+  return a0 < b0 + b.bytes && b0 < a0 + a.bytes;
+}
+// Outputs may not overlap an input or another output: the kernels read their
+// inputs while they write their outputs.  Inputs may overlap each other
+// (q == k == v is a valid self-attention call).
+inline int check_no_overlap(const char* fn, std::initializer_list<ArgSpan> inputs,
+                            std::initializer_list<ArgSpan> outputs) {
+  for (auto o = outputs.begin(); o != outputs.end(); ++o) {
+    for (const ArgSpan& i : inputs)
+      if (spans_overlap(*o, i))
+        return fail(TT_ERR_ARG, std::string(fn) + ": output " + o->name + " overlaps input " + i.name);
+    for (auto o2 = outputs.begin(); o2 != o; ++o2)
+      if (spans_overlap(*o, *o2))
+        return fail(TT_ERR_ARG, std::string(fn) + ": outputs " + o2->name + " and " + o->name + " overlap");
+  }
   return TT_OK;
 }
 

@@ -422,6 +422,49 @@ def test_errors_are_reported(capi):
         capi.lib().call("tt_attn_fwd_f32", None, None, None, None, None, 1, 1, 8, 8, 64, 0.1, 0, None)
 
 
+def test_overlapping_outputs_are_refused(capi):
+    """An output whose bytes overlap an input's or another output's is
+    refused before anything is launched; inputs may overlap each other
+    (q = k = v).  Every pointer lies inside an allocation of its size."""
+    import ctypes as C
+
+    L = capi.lib()
+    B, H, Lq, d = 1, 2, 64, 64
+    shp = (B, H, Lq, d)
+    big = capi.DeviceBuffer((2,) + shp, "bf16")  # room for two tensors
+    half = big.nbytes // 2
+    k, v, do = (capi.DeviceBuffer(shp, "bf16") for _ in range(3))
+    for i, b in enumerate((big, k, v, do)):
+        b.fill_normal(90 + i)
+    lse = capi.DeviceBuffer(shp[:3], "f32")
+    s = C.c_float(0.125)
+
+    def fwd(q, k_, v_, o, l):
+        return L.lib.tt_attn_fwd_bf16(q, k_, v_, o, l, B, H, Lq, Lq, d, s, 0, None)
+
+    assert fwd(big.ptr, k.ptr, v.ptr, big.ptr + half // 2, lse.ptr) == capi.TT_ERR_ARG
+    assert "output o overlaps input q" in L.last_error()
+    assert fwd(big.ptr, k.ptr, v.ptr, big.ptr + half, big.ptr + half + 64) == capi.TT_ERR_ARG
+    assert "outputs o and lse overlap" in L.last_error()
+    q32 = capi.DeviceBuffer((1, 1, 8, 32), "f32")
+    assert L.lib.tt_attn_fwd_f32(q32.ptr, k.ptr, v.ptr, big.ptr, q32.ptr + 64, 1, 1, 8, 8, 32, s, 0, None) \
+        == capi.TT_ERR_ARG
+    assert "output lse overlaps input q" in L.last_error()
+    # q = k = v is a valid self-attention call; o right after q in one block
+    assert fwd(big.ptr, big.ptr, big.ptr, big.ptr + half, lse.ptr) == capi.TT_OK, L.last_error()
+    L.sync()
+    o = big.ptr + half
+    assert L.lib.tt_attn_bwd_bf16(big.ptr, k.ptr, v.ptr, o, lse.ptr, do.ptr, k.ptr, v.ptr, do.ptr,
+                                  B, H, Lq, Lq, d, s, 0, None) == capi.TT_ERR_ARG
+    assert "output dQ overlaps input k" in L.last_error()
+    assert L.lib.tt_attn_bwd_bf16(k.ptr, k.ptr, k.ptr, k.ptr, lse.ptr, k.ptr, big.ptr, big.ptr + half - 2, do.ptr,
+                                  B, H, Lq, Lq, d, s, 0, None) == capi.TT_ERR_ARG
+    assert "outputs dQ and dK overlap" in L.last_error()
+    q1 = capi.DeviceBuffer((B, H, 1, d), "bf16")
+    assert L.lib.tt_attn_decode_bf16(q1.ptr, k.ptr, v.ptr, v.ptr + 128, None, B, H, Lq, d, s, None) == capi.TT_ERR_ARG
+    assert "output o overlaps input v" in L.last_error()
+
+
 def orc_golden(name):
     import os
 

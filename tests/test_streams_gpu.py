@@ -157,17 +157,17 @@ import ctypes as C, sys
 sys.path.insert(0, sys.argv[1])
 import tt_capi as T
 L = T.lib()
-ok = [T.DeviceBuffer((4, 256, 64), "bf16") for _ in range(6)]     # allocations 0..5 succeed
+ok = [T.DeviceBuffer((4, 256, 64), "bf16") for _ in range(8)]     # allocations 0..7 succeed
 p = C.c_void_p()
-rc = L.lib.tt_malloc(C.byref(p), 1 << 20)                          # allocation 6: refused
+rc = L.lib.tt_malloc(C.byref(p), 1 << 20)                          # allocation 8: refused
 assert rc == T.TT_ERR_NOMEM, rc
 assert "failure injection" in L.last_error(), L.last_error()
-q, k, v, do, o, g = ok[0], ok[1], ok[2], ok[3], ok[4], ok[5]
+q, k, v, do, o, gq, gk, gv = ok
 for b in ok:
     b.zero()
-lse = None
 # the backward needs a workspace buffer (a new allocation): refused cleanly
-rc = L.lib.tt_attn_bwd_bf16(q.ptr, k.ptr, v.ptr, o.ptr, o.ptr, do.ptr, g.ptr, g.ptr, g.ptr,
+# (the fp32 LSE rows, all zero, are read from the start of o's buffer)
+rc = L.lib.tt_attn_bwd_bf16(q.ptr, k.ptr, v.ptr, o.ptr, o.ptr, do.ptr, gq.ptr, gk.ptr, gv.ptr,
                             1, 4, 256, 256, 64, C.c_float(0.125), 1, None)
 assert rc == T.TT_ERR_NOMEM, (rc, L.last_error())
 # a forward needs no allocation: still works after the failures
@@ -179,7 +179,7 @@ print("CHILD_OK")
 
 
 def test_allocation_failure_injection(capi):
-    env = dict(os.environ, TT_FAIL_ALLOC_AFTER="6")
+    env = dict(os.environ, TT_FAIL_ALLOC_AFTER="8")
     r = subprocess.run([sys.executable, "-c", CHILD, os.path.join(ROOT, "pku-aiprogramming_amd")],
                        capture_output=True, text=True, timeout=120, env=env)
     _say(r.stdout[-500:] + r.stderr[-2000:])
