@@ -168,6 +168,11 @@ int tt_fill_normal(int dtype, void* dst, int64_t n, uint64_t seed, float scale, 
 
 /* ------------------------------------------------------------- attention */
 
+/* For every attention launcher below: an output whose bytes overlap an
+ * input's or another output's is refused with TT_ERR_ARG before anything is
+ * launched (the kernels read their inputs while writing their outputs);
+ * inputs may overlap each other (q == k == v is a valid call). */
+
 /* Forward: O = softmax(scale * Q K^T + M) V, LSE = rowwise log-sum-exp of the
  * scaled, masked scores (natural log).  M is the strict upper triangle
  * (key j > query i, top-left aligned) when causal != 0, else nothing.
