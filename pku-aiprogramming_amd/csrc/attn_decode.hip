@@ -6,8 +6,8 @@
 // HBM bandwidth and is built to stream K and V exactly once.
 //
 // Split-KV: workgroup id = bh * nsplit + split owns keys [split*chunk, (split+1)*chunk)
-// of one head.  Phase 1 streams its K rows (16-byte loads, TPR threads per
-// row, several rows in flight per thread) and writes the log2-domain scores
+// of one head.  Phase 1 streams its K rows (16-byte non-temporal loads, TPR
+// threads per row, several rows in flight per thread) and writes the log2-domain scores
 // to LDS; phase 2 reduces max and sum over the chunk; phase 3 streams the V
 // rows and accumulates sum_j p_j V_j.  Each split writes a normalised partial
 // (o_c, lse_c) in fp32; a combine kernel merges them by LSE rescaling:
@@ -94,7 +94,7 @@ __global__ __launch_bounds__(DEC_THREADS) void attn_decode_split_kernel(
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) {
       const int j = j0 + u * RPP;
-      kv[u] = j < n ? ldg16(Kh + (int64_t)j * D) : uint4{0, 0, 0, 0};
+      kv[u] = j < n ? ldg16_stream(Kh + (int64_t)j * D) : uint4{0, 0, 0, 0};
     }
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) {
@@ -132,7 +132,7 @@ __global__ __launch_bounds__(DEC_THREADS) void attn_decode_split_kernel(
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) {
       const int j = j0 + u * RPP;
-      vv[u] = j < n ? ldg16(Vh + (int64_t)j * D) : uint4{0, 0, 0, 0};
+      vv[u] = j < n ? ldg16_stream(Vh + (int64_t)j * D) : uint4{0, 0, 0, 0};
     }
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) {
