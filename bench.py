@@ -153,6 +153,8 @@ def run_decode(T, steps, warmup):
     for _ in range(warmup):
         T.attn_decode(q, k, v, o, lse, scale)
     T.lib().sync()
+    # one launch per step when a split covers a whole head (c4), else the split
+    # kernel and the combine kernel
     names = ["attn_decode_split", "attn_decode_combine"]
     marks = [[T.Event() for _ in range(3)] for _ in range(steps)]
     start, stop = T.Event(), T.Event()
@@ -161,10 +163,12 @@ def run_decode(T, steps, warmup):
         marks[s][0].record()
         T.set_launch_events(marks[s][1:])
         T.attn_decode(q, k, v, o, lse, scale)
+        launches = T.launch_events_recorded()
     stop.record()
     T.lib().sync()
     T.set_launch_events([])
     total_ms = T.Event.elapsed(start, stop)
+    names = names[:launches]
     per = {n: sum(T.Event.elapsed(marks[s][i], marks[s][i + 1]) for s in range(steps)) / steps
            for i, n in enumerate(names)}
     # The read rate this hardware gives a plain streaming kernel over the same

@@ -128,10 +128,14 @@ int tt_event_destroy(void* ev);
  * kernel launch, for i < n; later launches record nothing.  n = 0 (or
  * evs = NULL) disables it.  The events must stay alive until recorded. */
 int tt_set_launch_events(void** evs, int n);
+/* How many of those events the launches since tt_set_launch_events have
+ * recorded (a step whose kernel count depends on the shape, such as the
+ * decode with one or two launches, is timed by the events it recorded). */
+int tt_launch_events_recorded(int* n);
 
 /* Benchmark instrumentation (no counterpart in the reference): streams
  * `bytes` bytes of device memory at `buf` (16-byte aligned, bytes a multiple
- * of 16) with 16-byte loads, one contiguous 256 KiB run per workgroup, and
+ * of 16) with 16-byte non-temporal loads, one contiguous 256 KiB run per workgroup, and
  * stores nothing (out, one float, is written only if the data sums to a
  * sentinel).  It gives the HBM read rate that the decode kernel, which also
  * streams K and V once, is compared against. */

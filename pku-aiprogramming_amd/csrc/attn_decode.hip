@@ -12,6 +12,8 @@
 // rows and accumulates sum_j p_j V_j.  Each split writes a normalised partial
 // (o_c, lse_c) in fp32; a combine kernel merges them by LSE rescaling:
 //   lse = log2 sum_c 2^lse_c,  o = sum_c 2^(lse_c - lse) o_c.
+// When one split covers a whole head, the split kernel writes o and lse
+// itself and there is no combine launch.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -22,7 +24,10 @@
 namespace tt {
 
 constexpr int DEC_THREADS = 256;
-constexpr int DEC_MAX_CHUNK = 1024;  // keys per split (LDS score buffer)
+// Keys per split: the split kernel keeps the chunk's scores in LDS, and is
+// built for chunks up to 1024 keys (4 KB of scores) and up to 8192 (32 KB).
+constexpr int DEC_SMALL_CHUNK = 1024;
+constexpr int DEC_MAX_CHUNK = 8192;
 
 template <typename T> struct Vec16;  // 16 bytes of T as floats
 template <> struct Vec16<u16> {
@@ -63,15 +68,18 @@ __device__ __forceinline__ float block_reduce(float v, float* red, bool is_max) 
   return r;
 }
 
-template <typename T, int D, int UNROLL>
+// MAXC: largest chunk the LDS score buffer holds.  DIRECT (nsplit == 1): o
+// and lse (natural log, may be null) are written here in the output type;
+// otherwise the fp32 partials go to part_o / part_lse.
+template <typename T, int D, int UNROLL, int MAXC, bool DIRECT>
 __global__ __launch_bounds__(DEC_THREADS) void attn_decode_split_kernel(
     const T* __restrict__ q, const T* __restrict__ K, const T* __restrict__ V,
-    float* __restrict__ part_o, float* __restrict__ part_lse, int Lkv, int nsplit, int chunk,
-    float sl2) {
+    float* __restrict__ part_o, float* __restrict__ part_lse, T* __restrict__ o, float* __restrict__ lse,
+    int Lkv, int nsplit, int chunk, float sl2) {
   constexpr int EPT = Vec16<T>::N;     // elements per 16-byte load
   constexpr int TPR = D / EPT;         // threads per key row
   constexpr int RPP = DEC_THREADS / TPR;  // rows per pass
-  __shared__ float sS[DEC_MAX_CHUNK];
+  __shared__ float sS[MAXC];
   __shared__ float sAcc[RPP * D];
   __shared__ float red[DEC_THREADS / 64];
 
@@ -153,9 +161,19 @@ __global__ __launch_bounds__(DEC_THREADS) void attn_decode_split_kernel(
     float s = 0.f;
 #pragma unroll 8
     for (int r = 0; r < RPP; ++r) s += sAcc[r * D + dd];
-    part_o[pidx * D + dd] = s * inv;
+    if constexpr (!DIRECT)
+      part_o[pidx * D + dd] = s * inv;
+    else if constexpr (sizeof(T) == 2)
+      o[bh * D + dd] = f32_to_bf16(s * inv);
+    else
+      o[bh * D + dd] = s * inv;
   }
-  if (tid == 0) part_lse[pidx] = mx + __log2f(sm);
+  if (tid == 0) {
+    if constexpr (!DIRECT)
+      part_lse[pidx] = mx + __log2f(sm);
+    else if (lse)
+      lse[bh] = (mx + __log2f(sm)) * kLn2;
+  }
 }
 
 // One workgroup of D threads per (b, h): merge the nsplit partials.
@@ -186,15 +204,33 @@ __global__ __launch_bounds__(D) void attn_decode_combine_kernel(const float* __r
 template <typename T, int D>
 static int launch_decode(const T* q, const T* k, const T* v, T* o, float* lse, int64_t BH, int64_t Lkv,
                          float scale, hipStream_t st) {
-  // Split size: enough workgroups to cover the 256 CUs several times over while
-  // each split streams as many rows as that allows (1024-key splits measured
-  // 1.3 % faster than 512-key ones at B=64 H=32 Lkv=8192).
-  auto splits = [&](int c) { return BH * ((Lkv + c - 1) / c); };
-  int chunk = splits(1024) >= 4096 ? 1024 : splits(512) >= 2048 ? 512 : 256;
+  // Split size: the longest split (fewer workgroups, each streaming more rows)
+  // that still leaves >= 2048 workgroups, 8 per CU; else 256 keys.  At
+  // B=64 H=32 Lkv=8192 (2048 heads) one split per head streams K/V at
+  // 1.208 ms, against 1.232 / 1.244 / 1.259 / 1.301 ms for 4096 / 2048 /
+  // 1024 / 512-key splits.
+  auto splits = [&](int64_t c) { return BH * ((Lkv + c - 1) / c); };
+  int chunk = 256;
+  for (int c = DEC_MAX_CHUNK; c >= 512; c >>= 1)
+    if (splits(c) >= 2048) {
+      chunk = c;
+      break;
+    }
   if (Lkv < chunk) chunk = (int)((Lkv + 63) / 64 * 64);
-  if (chunk > DEC_MAX_CHUNK) chunk = DEC_MAX_CHUNK;
   const int64_t nsplit = (Lkv + chunk - 1) / chunk;
   if (BH * nsplit > 0x7fffffff) return fail(TT_ERR_ARG, "attention decode: grid too large");
+  const float sl2 = scale * kLog2e;
+  const dim3 grid((unsigned)(nsplit * BH)), block(DEC_THREADS);
+  if (nsplit == 1) {  // one split per head: no partials, no combine
+    if (chunk <= DEC_SMALL_CHUNK)
+      hipLaunchKernelGGL((attn_decode_split_kernel<T, D, 8, DEC_SMALL_CHUNK, true>), grid, block, 0, st, q, k, v,
+                         nullptr, nullptr, o, lse, (int)Lkv, 1, chunk, sl2);
+    else
+      hipLaunchKernelGGL((attn_decode_split_kernel<T, D, 8, DEC_MAX_CHUNK, true>), grid, block, 0, st, q, k, v,
+                         nullptr, nullptr, o, lse, (int)Lkv, 1, chunk, sl2);
+    TT_LAUNCHED("attention decode launch", st);
+    return ok();
+  }
   void* ws = nullptr;
   const size_t need = (size_t)(BH * nsplit) * (D + 1) * sizeof(float);
   WorkspaceLease lease;  // held until both kernels are launched
@@ -202,9 +238,12 @@ static int launch_decode(const T* q, const T* k, const T* v, T* o, float* lse, i
   if (rc) return rc;
   float* part_o = (float*)ws;
   float* part_lse = part_o + BH * nsplit * D;
-  hipLaunchKernelGGL((attn_decode_split_kernel<T, D, 8>), dim3((unsigned)(nsplit * BH)),
-                     dim3(DEC_THREADS), 0, st, q, k, v, part_o, part_lse, (int)Lkv, (int)nsplit, chunk,
-                     scale * kLog2e);
+  if (chunk <= DEC_SMALL_CHUNK)
+    hipLaunchKernelGGL((attn_decode_split_kernel<T, D, 8, DEC_SMALL_CHUNK, false>), grid, block, 0, st, q, k, v,
+                       part_o, part_lse, nullptr, nullptr, (int)Lkv, (int)nsplit, chunk, sl2);
+  else
+    hipLaunchKernelGGL((attn_decode_split_kernel<T, D, 8, DEC_MAX_CHUNK, false>), grid, block, 0, st, q, k, v,
+                       part_o, part_lse, nullptr, nullptr, (int)Lkv, (int)nsplit, chunk, sl2);
   TT_LAUNCHED("attention decode split launch", st);
   hipLaunchKernelGGL((attn_decode_combine_kernel<T, D>), dim3((unsigned)BH), dim3(D), 0, st, part_o,
                      part_lse, o, lse, (int)nsplit);

@@ -405,6 +405,13 @@ int tt_set_launch_events(void** evs, int n) {
   return TT_OK;
 }
 
+int tt_launch_events_recorded(int* n) {
+  if (!n) return fail(TT_ERR_ARG, "tt_launch_events_recorded: null pointer");
+  std::lock_guard<std::mutex> lk(g_ev_mu);
+  *n = (int)g_launch_next;
+  return TT_OK;
+}
+
 // Streams chunk16 16-byte words per workgroup (workgroup b: words
 // [b * chunk16, min((b + 1) * chunk16, n16))), 16 non-temporal loads in
 // flight per thread (the fastest streaming-read pattern measured on the

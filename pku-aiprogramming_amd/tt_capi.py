@@ -54,6 +54,7 @@ _SIGS = {
     "tt_event_elapsed_ms": (C.c_int, [C.POINTER(C.c_float), _p, _p]),
     "tt_event_destroy": (C.c_int, [_p]),
     "tt_set_launch_events": (C.c_int, [C.POINTER(_p), C.c_int]),
+    "tt_launch_events_recorded": (C.c_int, [C.POINTER(C.c_int)]),
     "tt_read_probe": (C.c_int, [_p, _i64, _p, _p]),
     "tt_elementwise": (C.c_int, [C.c_int, C.c_int, _p, _p, _p, _i64, C.c_double, C.c_double, C.c_uint64, _p]),
     "tt_fill_normal": (C.c_int, [C.c_int, _p, _i64, C.c_uint64, C.c_float, _p]),
@@ -318,6 +319,13 @@ def set_launch_events(events: Sequence[Event]):
     (instrumentation for per-kernel timing); [] disables it."""
     arr = (C.c_void_p * max(1, len(events)))(*[e.ptr for e in events])
     lib().call("tt_set_launch_events", arr, len(events))
+
+
+def launch_events_recorded() -> int:
+    """How many events set by set_launch_events have been recorded so far."""
+    n = C.c_int(0)
+    lib().call("tt_launch_events_recorded", C.byref(n))
+    return n.value
 
 
 class Timer:

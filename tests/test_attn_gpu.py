@@ -258,14 +258,23 @@ def test_long_sequence_few_heads_bf16(capi):
     _check("head 1 dV", dv[:, 1:2], rv, TOL["bf16"])
 
 
+DECODE_LONG_SPLITS = [
+    # (B, H, Lkv, d): 512 heads -> five 2048-key splits per head, the last one
+    # partial (808 keys), merged by the combine kernel
+    (8, 64, 9000, 64),
+    # 2048 heads -> one 3000-key split per head, written directly (no combine)
+    (64, 32, 3000, 64),
+]
+
+
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
-def test_decode_large_grid_ragged_last_split(capi, dtype):
-    """A grid large enough for the 1024-key splits, with a partial last split
-    (Lkv = 9000): every head against the forward kernel run with Lq = 1, and
+@pytest.mark.parametrize("B,H,Lkv,d", DECODE_LONG_SPLITS)
+def test_decode_large_grid_ragged_last_split(capi, dtype, B, H, Lkv, d):
+    """Grids large enough for splits longer than 1024 keys, ragged in their
+    last split: every head against the forward kernel run with Lq = 1, and
     sampled heads against the oracle."""
-    B, H, Lkv, d = 8, 64, 9000, 64
     scale = float(np.float32(1.0 / math.sqrt(d)))
-    _say(f"decode {dtype} B={B} H={H} Lkv={Lkv} d={d} (1024-key splits, ragged last)")
+    _say(f"decode {dtype} B={B} H={H} Lkv={Lkv} d={d} (long splits, ragged last)")
     q = capi.DeviceBuffer((B, H, 1, d), dtype)
     k = capi.DeviceBuffer((B, H, Lkv, d), dtype)
     v = capi.DeviceBuffer((B, H, Lkv, d), dtype)
@@ -285,7 +294,7 @@ def test_decode_large_grid_ragged_last_split(capi, dtype):
     qh = q.download()
     esz = 2 if dtype == "bf16" else 4
     import ctypes as C
-    for (bb, hh) in [(0, 0), (5, 37), (7, 63)]:
+    for (bb, hh) in [(0, 0), (B // 2 + 1, H // 2 + 5), (B - 1, H - 1)]:
         bh = bb * H + hh
         slab = Lkv * d
         raw = np.empty(slab, np.uint16 if dtype == "bf16" else np.float32)
