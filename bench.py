@@ -52,7 +52,7 @@ MEASURED_TRAFFIC_MIB = {
     "attn_fwd": 580.9,
     "attn_bwd_dq": 908.3,      # also the row pre-pass: reads O, writes -D and LSE log2(e)
     "attn_bwd_dkdv": 869.0,
-    "attn_decode_split": 8209.0,
+    "attn_decode_split": 8193.2,
     "softmax_reg": 2048.1,
     "gemm_bf16_nn": 2527.8 + 149.6,  # k_gemm_dma 8192^3 NN (profiles/gemm_kernel_stats.md)     # k_softmax_reg<16>, 262144 x 1024 fp32 (profiles/softmax_rows_kernel_stats.md)
 }
