@@ -29,8 +29,11 @@ CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 INCLUDE = os.path.join(ROOT, "include")
 
-HIP_SOURCES = ["tt_runtime.hip", "attn_fwd.hip", "attn_bwd.hip", "attn_decode.hip", "softmax.hip", "gemm.hip",
-               "staging.hip"]
+HIP_SOURCES = ["tt_runtime.hip", "attn_fwd.hip", "attn_bwd.hip", "attn_bwd_w64.hip", "attn_decode.hip", "softmax.hip",
+               "gemm.hip", "staging.hip"]
+# Per-file extra flags.  attn_bwd_w64.hip keeps its dK / dV accumulators in
+# AGPRs by inline asm and needs its builtin MFMAs (scores) to write VGPRs.
+HIP_FILE_FLAGS = {"attn_bwd_w64.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
 # Host-only C++ linked into libtt_hip.so (the staged transfers' copy loops).
 LIB_HOST_SOURCES = ["host_copy.cpp"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -82,7 +85,8 @@ def build(verbose: bool = False) -> dict:
 
     def hip_obj(src):
         obj = os.path.join(OBJ, src.replace(".hip", ".o"))
-        _run([HIPCC, *HIP_FLAGS, "-I", INCLUDE, "-c", os.path.join(CSRC, src), "-o", obj], verbose)
+        _run([HIPCC, *HIP_FLAGS, *HIP_FILE_FLAGS.get(src, []), "-I", INCLUDE, "-c", os.path.join(CSRC, src), "-o", obj],
+             verbose)
         return obj
 
     py_inc = sysconfig.get_paths()["include"]

@@ -22,8 +22,10 @@
 //         loops over key tiles: S^T and dP^T from K / V row reads,
 //         dQ^T += K^T dS^T from transpose reads of the same K tile.
 // bf16 at d >= 64: the dq kernel (attn_bwd_dq_pipe_kernel) runs first and
-// also writes the rows -D and LSE log2(e) the dkdv kernel reads; d = 32 runs
-// a separate row pre-pass (attn_bwd_delta_kernel), then dkdv, then dq.  fp32
+// also writes the rows -D and LSE log2(e) the dkdv kernel reads; at d = 128
+// the dK / dV role runs one wave per SIMD with 64 keys per wave
+// (attn_bwd_w64.hip), at d = 64 the kernel below.  d = 32 runs a separate
+// row pre-pass (attn_bwd_delta_kernel), then dkdv, then dq.  fp32
 // (attn_bwd_f32.h): the pre-pass, then one launch holding both roles.
 // All bf16 tiles are filled by direct global->LDS loads.  Loads past the end
 // of a sequence read a clamped (valid) row and the result is masked, so the
@@ -727,6 +729,11 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_pipe_kernel(
 }
 
 // ------------------------------------------------------------------ launchers
+// dK / dV at d = 128 with one wave per SIMD (attn_bwd_w64.hip).
+int launch_dkdv_w64(const u16* q, const u16* k, const u16* v, const u16* dout, const float* l2, const float* nd,
+                    u16* dk, u16* dv, int64_t BH, int64_t Lq, int64_t Lk, float sl2, float scale, bool causal,
+                    hipStream_t st);
+
 // `delta`: device scratch of 2 * BH * Lq floats that the kernels of this call
 // own until they finish: -D (negated row sums of dO o O), then LSE * log2(e).
 template <typename T, int D, bool CAUSAL>
@@ -747,6 +754,8 @@ static int launch_bwd(const T* q, const T* k, const T* v, const T* o, const floa
     hipLaunchKernelGGL((attn_bwd_dq_pipe_kernel<D, CAUSAL>), dim3((unsigned)(nqp * BH)), dim3(256), 0, st, q, k, v, o,
                        dout, lse, l2, delta, dq, (int)Lq, (int)Lk, (int)BH, (int)nqp, gp, sl2, scale);
     TT_LAUNCHED("attention backward dQ launch", st);
+    if constexpr (D == 128)
+      return launch_dkdv_w64(q, k, v, dout, l2, delta, dk, dv, BH, Lq, Lk, sl2, scale, CAUSAL, st);
     hipLaunchKernelGGL((attn_bwd_dkdv_bf16_kernel<D, CAUSAL>), dim3((unsigned)(nkt * BH)), dim3(64 * NW), 0, st, q,
                        k, v, dout, l2, delta, dk, dv, (int)Lq, (int)Lk, (int)BH, (int)nkt, gk, sl2, scale);
     TT_LAUNCHED("attention backward dK/dV launch", st);

@@ -243,6 +243,16 @@ struct TileDma {
     glds16(src + (int64_t)row0 * D + (int64_t)D * kStep * (i - i % kPh), voff[i % kPh],
            lds_addr(dst) + 1024u * (uint32_t)(w + NW * i));
   }
+  // Load instruction i (0 <= i < kLoads) alone of issue(src, row0, rmax,
+  // dst), always by the clamped form (no branch), for kernels that spread a
+  // tile's loads over their compute.  Requires 0 <= row0 < rmax.
+  __device__ __forceinline__ void issue_part_clamped(const u16* src, int row0, int rmax, const u16* dst, int i) const {
+    const int p0 = w * 64 + (threadIdx.x & 63);
+    const int r0 = p0 / kCPR;
+    const int ch = (p0 % kCPR) ^ SwzTile<D>::sw(r0 + i * kStep);
+    const int row = min(r0 + i * kStep, rmax - 1 - row0);
+    glds16(src + (int64_t)row0 * D, 2u * (uint32_t)(row * D + 8 * ch), lds_addr(dst) + 1024u * (uint32_t)(w + NW * i));
+  }
   // Issue the loads of rows [row0, row0 + ROWS) of `src` into the tile at
   // `dst`.  Requires 0 <= row0 < rmax; rows >= rmax read row rmax - 1 instead
   // (callers mask them).  Completion: a vmcnt wait, then a barrier.

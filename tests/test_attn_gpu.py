@@ -323,6 +323,12 @@ SHAPES = [
     (2, 1, 512, 512, 128, True),
     (1, 1, 128, 512, 128, False),
     (2, 1, 384, 256, 128, False),
+    # d = 128 bf16 dK / dV: 256-key workgroups (two 32-key halves per wave), 32-query tiles
+    (1, 1, 33, 33, 128, True),      # one key block, ragged query tile on the diagonal
+    (1, 2, 300, 300, 128, True),    # second key block of 44 keys, ragged last query tile
+    (2, 1, 257, 513, 128, False),   # last key block holds one key
+    (1, 1, 96, 40, 128, False),     # fewer keys than one wave's first half
+    (1, 1, 544, 544, 128, True),    # a last key block of exactly one 32-key half
 ]
 
 
