@@ -78,6 +78,9 @@ constexpr int DKW_BN = 256, DKW_BQ = 32, DKW_STAGES = 4;
 #endif
 static_assert(DKW_READ_AHEAD % 2 == 0 && DKW_READ_AHEAD >= 2 && DKW_READ_AHEAD <= 12, "read-ahead in whole dP slot pairs");
 
+// Bytes of the kernel's LDS block: Q and dO rings, LSE / -D rows, V rows.
+constexpr int kDkwLds = 2 * DKW_STAGES * 2 * DKW_BQ * 128 + 2 * 4 * DKW_STAGES * 64 + 2 * DKW_BN * 128;
+
 // f(integral_constant<int, I>) for I = B .. E - 1, in order, inlined.
 template <int B, int E, typename F>
 __device__ __forceinline__ void static_for(F&& f) {
@@ -87,11 +90,40 @@ __device__ __forceinline__ void static_for(F&& f) {
   }
 }
 
+// Static schedule of the persistent kernel: item `round` of workgroup b of G,
+// as (key block kt, head bh); false when b has no more items.  With P > 0
+// (BH % 8 == 0, G = 8 W): workgroup b runs on XCD b % 8 (consecutive
+// workgroup ids go round-robin over the 8 XCDs), which owns heads
+// x + 8 i; its items are taken P heads at a time (their K / V and Q / dO
+// stay in that XCD's L2), within a group heaviest key block first, and
+// dealt out snake-wise -- round r gives the XCD's W workgroups the next W
+// items in forward order for even r and backward for odd r -- so that under a
+// causal mask every workgroup pairs heavy with light blocks (at c5 each of
+// the 256 workgroups gets exactly 544 query tiles).  P = 0: the same over
+// all items, heads interleaved.
+__device__ __forceinline__ bool sched_item(int b, int G, int round, int nkt, int BH, int P, int& kt, int& bh) {
+  if (P > 0) {
+    const int x = b & 7, W = G >> 3, j = b >> 3;
+    const int idx = round * W + ((round & 1) ? W - 1 - j : j);
+    if (idx >= (BH >> 3) * nkt) return false;
+    const int gsz = P * nkt;
+    const int gi = idx / gsz, e = idx - gi * gsz;
+    kt = e / P;
+    bh = x + 8 * (gi * P + (e - kt * P));
+  } else {
+    const int idx = round * G + ((round & 1) ? G - 1 - b : b);
+    if (idx >= nkt * BH) return false;
+    kt = idx / BH;
+    bh = idx - kt * BH;
+  }
+  return true;
+}
+
 template <bool CAUSAL>
-__global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_w64_kernel(
-    const u16* __restrict__ Q, const u16* __restrict__ K, const u16* __restrict__ V,
-    const u16* __restrict__ dO, const float* __restrict__ L2, const float* __restrict__ NDelta,
-    u16* __restrict__ dK, u16* __restrict__ dV, int Lq, int Lk, int BH, int nkt, int group, float sl2,
+__device__ __forceinline__ void dkdv_w64_item(
+    char* smem, const int kt, const int bh, const u16* __restrict__ Q, const u16* __restrict__ K,
+    const u16* __restrict__ V, const u16* __restrict__ dO, const float* __restrict__ L2,
+    const float* __restrict__ NDelta, u16* __restrict__ dK, u16* __restrict__ dV, int Lq, int Lk, float sl2,
     float scale) {
   constexpr int D = 128, NW = 4, BN = DKW_BN, BQ = DKW_BQ, S = DKW_STAGES, NC = D / 16, ND = D / 32;
   using Tile = SwzTile<D>;
@@ -107,18 +139,20 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_w64_kernel(
                 kLds = kOV + 2 * Tile::kElems(BN);
   constexpr int kVHalf = 2 * 128 * D;  // bytes between a wave's two V halves
   static_assert(kOdO - kOQ + (S - 1) * TB + TB <= 65536, "ring offsets exceed the LDS immediate");
-  __shared__ __align__(16) char smem[kLds];
+  static_assert(kLds <= kDkwLds, "LDS block");
   u16* const sQ = reinterpret_cast<u16*>(smem + kOQ);
   u16* const sdO = reinterpret_cast<u16*>(smem + kOdO);
   float* const sL = reinterpret_cast<float*>(smem + kOL);
   float* const sDl = reinterpret_cast<float*>(smem + kOD);
   u16* const sV = reinterpret_cast<u16*>(smem + kOV);
-  const uint32_t a0 = lds_addr(smem);
-
-  const int l = threadIdx.x & 63, g = l >> 5, r32 = l & 31;
+  // The lane's LDS addresses are recomputed for every item (from opaque
+  // copies of the base and the lane id): hoisted out of the persistent loop,
+  // they would stay live across the epilogue and prologue and spill.
+  uint32_t a0 = lds_addr(smem), tid = threadIdx.x;
+  opaque(a0);
+  opaque(tid);
+  const int l = tid & 63, g = l >> 5, r32 = l & 31;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  int kt, bh;
-  map_tile(blockIdx.x, nkt, BH, group, kt, bh, false);  // causal: key tile 0 sees every query
   const int k0 = kt * BN;
   const int key0 = k0 + 32 * w + r32, key1 = key0 + 128;
   const int64_t qbase = (int64_t)bh * Lq * D;
@@ -429,26 +463,58 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_w64_kernel(
   wait_vmem_le<0>();  // nothing may be in flight into LDS when the workgroup exits
   agpr_drain(adk, adv);
 
+  // Epilogue through LDS: the rows dK (scaled) and dV of the workgroup's 256
+  // keys go to LDS as bf16 (SwzTile layout, dK rows 0-255 then dV rows
+  // 256-511), then every lane stores whole 16-byte chunks, so one store
+  // instruction writes four contiguous 256-byte rows.  Stored straight from
+  // the accumulators (8 bytes per lane into 32 different rows) the epilogue
+  // took about 10 us per workgroup at c5.
+  static_assert(kLds >= 2 * 2 * Tile::kElems(BN), "LDS block too small for the staged epilogue");
+  __syncthreads();  // every wave is done with the ring and the V rows
+  u16* const stage = reinterpret_cast<u16*>(smem);
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
-    const int key = h == 0 ? key0 : key1;
+    const int row = 32 * w + 128 * h + r32;
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; r += 4) {
+        const int d0 = 32 * dt + acc_row(r, g);
+        uint2 a, bb;
+        a.x = pack_bf16x2(adk[h][dt][r] * scale, adk[h][dt][r + 1] * scale);
+        a.y = pack_bf16x2(adk[h][dt][r + 2] * scale, adk[h][dt][r + 3] * scale);
+        bb.x = pack_bf16x2(adv[h][dt][r], adv[h][dt][r + 1]);
+        bb.y = pack_bf16x2(adv[h][dt][r + 2], adv[h][dt][r + 3]);
+        *reinterpret_cast<uint2*>(&stage[Tile::at4(row, d0)]) = a;
+        *reinterpret_cast<uint2*>(&stage[Tile::at4(BN + row, d0)]) = bb;
+      }
+  }
+  __syncthreads();
+  constexpr int CPR = D / 8;  // 16-byte chunks per row
+#pragma unroll 4
+  for (int c = threadIdx.x; c < 2 * BN * CPR; c += 64 * NW) {
+    const int row = c / CPR, ch = c % CPR;
+    const int key = k0 + (row & (BN - 1));
     if (key < Lk) {
-      u16* dkrow = dK + kbase + (int64_t)key * D;
-      u16* dvrow = dV + kbase + (int64_t)key * D;
-#pragma unroll
-      for (int dt = 0; dt < ND; ++dt)
-#pragma unroll
-        for (int r = 0; r < 16; r += 4) {
-          const int d0 = 32 * dt + acc_row(r, g);
-          uint2 a, bb;
-          a.x = pack_bf16x2(adk[h][dt][r] * scale, adk[h][dt][r + 1] * scale);
-          a.y = pack_bf16x2(adk[h][dt][r + 2] * scale, adk[h][dt][r + 3] * scale);
-          bb.x = pack_bf16x2(adv[h][dt][r], adv[h][dt][r + 1]);
-          bb.y = pack_bf16x2(adv[h][dt][r + 2], adv[h][dt][r + 3]);
-          *reinterpret_cast<uint2*>(dkrow + d0) = a;
-          *reinterpret_cast<uint2*>(dvrow + d0) = bb;
-        }
+      const uint4 v = *reinterpret_cast<const uint4*>(&stage[Tile::chunk(row, ch)]);
+      *reinterpret_cast<uint4*>((row < BN ? dK : dV) + kbase + (int64_t)key * D + 8 * ch) = v;
     }
+  }
+}
+
+// Persistent kernel: G workgroups (at most one per CU, so all run at once),
+// each working through its items of sched_item.
+template <bool CAUSAL>
+__global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_w64_kernel(
+    const u16* __restrict__ Q, const u16* __restrict__ K, const u16* __restrict__ V,
+    const u16* __restrict__ dO, const float* __restrict__ L2, const float* __restrict__ NDelta,
+    u16* __restrict__ dK, u16* __restrict__ dV, int Lq, int Lk, int BH, int nkt, int P, float sl2,
+    float scale) {
+  __shared__ __align__(16) char smem[kDkwLds];
+  int kt, bh;
+  for (int round = 0; sched_item(blockIdx.x, gridDim.x, round, nkt, BH, P, kt, bh); ++round) {
+    if (round > 0) __syncthreads();  // the previous item's epilogue reads of LDS are done
+    dkdv_w64_item<CAUSAL>(smem, kt, bh, Q, K, V, dO, L2, NDelta, dK, dV, Lq, Lk, sl2, scale);
   }
 }
 
@@ -461,13 +527,16 @@ int launch_dkdv_w64(const u16* q, const u16* k, const u16* v, const u16* dout, c
                     hipStream_t st) {
   const int64_t nkt = (Lk + DKW_BN - 1) / DKW_BN;
   if (nkt * BH > 0x7fffffff) return fail(TT_ERR_ARG, "attention backward: grid too large");
-  const int gk = pick_group(BH, nkt, 32);
+  // one workgroup per CU (the LDS block allows no second), each through its share of the items
+  const int64_t cus = device_cu_count(), items = nkt * BH;
+  const int G = (int)(items < cus ? items : cus);
+  const int P = (G % 8 == 0 && G >= 64) ? pick_group(BH, nkt, G / 8) : 0;
   if (causal)
-    hipLaunchKernelGGL((attn_bwd_dkdv_w64_kernel<true>), dim3((unsigned)(nkt * BH)), dim3(256), 0, st, q, k, v,
-                       dout, l2, nd, dk, dv, (int)Lq, (int)Lk, (int)BH, (int)nkt, gk, sl2, scale);
+    hipLaunchKernelGGL((attn_bwd_dkdv_w64_kernel<true>), dim3((unsigned)G), dim3(256), 0, st, q, k, v, dout, l2,
+                       nd, dk, dv, (int)Lq, (int)Lk, (int)BH, (int)nkt, P, sl2, scale);
   else
-    hipLaunchKernelGGL((attn_bwd_dkdv_w64_kernel<false>), dim3((unsigned)(nkt * BH)), dim3(256), 0, st, q, k, v,
-                       dout, l2, nd, dk, dv, (int)Lq, (int)Lk, (int)BH, (int)nkt, gk, sl2, scale);
+    hipLaunchKernelGGL((attn_bwd_dkdv_w64_kernel<false>), dim3((unsigned)G), dim3(256), 0, st, q, k, v, dout, l2,
+                       nd, dk, dv, (int)Lq, (int)Lk, (int)BH, (int)nkt, P, sl2, scale);
   TT_LAUNCHED("attention backward dK/dV launch", st);
   return ok();
 }

@@ -21,6 +21,8 @@ int hip_fail(hipError_t e, const char* what);
 // The library stream (created by tt_init on first use).
 hipStream_t stream_or_default(void* s);
 int ensure_init();
+// Compute units of the bound device (after ensure_init).
+int device_cu_count();
 
 // Records the next instrumentation event (tt_set_launch_events) after a
 // kernel launch on `s`; a no-op unless instrumentation is enabled.

@@ -43,7 +43,10 @@ static std::mutex g_mu;
 // in place; read (acquire) without the lock on every call.
 static std::atomic<bool> g_inited{false};
 static int g_device = 0;
+static int g_cus = 1;  // compute units of the bound device (set by tt_init)
 static hipStream_t g_stream = nullptr;
+
+int device_cu_count() { return g_cus; }
 
 int ensure_init() {
   if (g_inited.load(std::memory_order_acquire)) return TT_OK;
@@ -272,6 +275,9 @@ int tt_init(int device) {
   void* sp = nullptr;
   TT_HIP(hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch)));
   g_scratch_ptr[device] = sp;
+  int cus = 0;
+  TT_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device));
+  g_cus = cus > 0 ? cus : 1;
   // Default priority on purpose: one stream, ordinary priority.
   TT_HIP(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
   g_device = device;
