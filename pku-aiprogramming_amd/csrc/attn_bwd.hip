@@ -48,15 +48,8 @@ namespace tt {
 constexpr int bwd_nw(int) { return 4; }
 constexpr int kBwdStages = 2;
 constexpr int DQ_BN = 64;  // keys per LDS tile of the d = 32 dQ kernel
-// Query rows per LDS tile of the dK/dV kernel: the ring of Q / dO tiles plus
-// the V rows of the workgroup fit 160 KB of LDS.
-constexpr int dkdv_bq(int D) { return D == 128 ? 32 : 64; }
-// K chunks (16 columns each) the dK/dV kernel keeps in LDS rather than in
-// registers.  At d = 128 the dK / dV accumulators (128 VGPRs) and the K rows
-// (32) leave too little of the 256 registers of a 2-waves-per-SIMD kernel;
-// each parked chunk frees 4 VGPRs for one extra 16-byte LDS read per query
-// tile.
-constexpr int dkdv_klds(int D) { return D == 128 ? 3 : 0; }
+// Query rows per LDS tile of the d <= 64 dK/dV kernel.
+constexpr int kDkdvBQ = 64;
 
 // ND_i = -D_i = -sum_d dO[i][d] * O[i][d], one 16-byte chunk per thread
 // (stored negated: the dK/dV kernel starts its dP accumulator at -D, so the
@@ -105,10 +98,9 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_b
     u16* __restrict__ dK, u16* __restrict__ dV, int Lq, int Lk, int BH, int nkt, int group, float sl2,
     float scale) {
   using Tile = SwzTile<D>;
-  constexpr int NW = bwd_nw(D), BN = 32 * NW, BQ = dkdv_bq(D), MT = BQ / 32, S = kBwdStages;
+  constexpr int NW = bwd_nw(D), BN = 32 * NW, BQ = kDkdvBQ, MT = BQ / 32, S = kBwdStages;
   constexpr int NC = D / 16, ND = D / 32;
-  constexpr int KL = dkdv_klds(D), KR = NC - KL;  // K chunks parked in LDS / held in registers
-  static_assert(KL >= 0 && KL <= NC, "bad K chunk split");
+  static_assert(D <= 64, "d = 128 runs the one-wave-per-SIMD kernel (attn_bwd_w64.hip)");
   constexpr int TE = Tile::kElems(BQ);
   constexpr int VS = 64;  // stride of the LSE / D row buffers (one 64-lane load each)
   using Dma = TileDma<D, BQ, NW>;
@@ -116,12 +108,9 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_b
   // One LDS block, carved at fixed byte offsets so that every operand read
   // is a per-lane address plus an immediate: the ring of Q / dO tiles with
   // their LSE (log2) / D rows and the workgroup's V rows, all filled by direct
-  // global->LDS loads, then the parked K chunks (lane-linear: chunk KR + c of
-  // lane l of wave w at 16 (64 (c NW + w) + l) bytes).
+  // global->LDS loads.  50 KB at d = 64 lets three workgroups share a CU.
   constexpr int kOQ = 0, kOdO = kOQ + 2 * S * TE, kOV = kOdO + 2 * S * TE, kOL = kOV + 2 * Tile::kElems(BN),
-                kOD = kOL + 4 * S * VS, kOK = kOD + 4 * S * VS, kLds = kOK + (KL > 0 ? KL * NW * 1024 : 16);
-  // (no parked K at d <= 64: 50 KB then lets three workgroups share a CU at
-  // d = 64, which a 54 KB block did not; the dK/dV kernel ran 8 % faster)
+                kOD = kOL + 4 * S * VS, kLds = kOD + 4 * S * VS;
   static_assert(kOV <= 65536, "Q / dO ring offsets exceed the 16-bit LDS immediate");
   __shared__ __align__(16) char smem[kLds];
   u16* const sQ = reinterpret_cast<u16*>(smem + kOQ);
@@ -129,7 +118,6 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_b
   u16* const sV = reinterpret_cast<u16*>(smem + kOV);
   float* const sL = reinterpret_cast<float*>(smem + kOL);
   float* const sDl = reinterpret_cast<float*>(smem + kOD);
-  u16* const sKf = reinterpret_cast<u16*>(smem + kOK);
   const uint32_t a0 = lds_addr(smem);
 
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63, g = l >> 5, r32 = l & 31;
@@ -150,9 +138,6 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_b
     for (int c = 0; c < NC; ++c)
       kf[c] = __builtin_bit_cast(bf16x8, ldg16(K + kbase + (int64_t)kr * D + 16 * c + 8 * g));
   }
-  // K operand of chunk c (each lane reads back only what it parked itself)
-  uint32_t kofs = a0 + kOK + 16 * (64 * w + l);
-  auto kop = [&](int c) { return c < KR ? kf[c] : lds_ld<bf16x8>(kofs + (c - KR) * NW * 1024); };
   f32x16 adk[ND], adv[ND];
 #pragma unroll
   for (int dt = 0; dt < ND; ++dt) adk[dt] = adv[dt] = f32x16{};
@@ -220,7 +205,7 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_b
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
         const uint32_t off = roff[c] + bq + 64 * mt * D;
-        s = mfma_bf16_32x32x16(lds_ld<bf16x8>(off), kop(c), s);
+        s = mfma_bf16_32x32x16(lds_ld<bf16x8>(off), kf[c], s);
         const bf16x8 vb = lds_ld<bf16x8>(voff[c]);
         dp = mfma_bf16_32x32x16(lds_ld<bf16x8>(off + (kOdO - kOQ)), vb, dp);
       }
@@ -298,9 +283,8 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_b
       opaque(troff[1][dt]);
     }
     opaque(lofs);
-    opaque(kofs);
     // LLVM's single-wave MFMA / LDS interleave strategy for the tile's
-    // scheduling region (1 % fewer cycles at d = 128)
+    // scheduling region
     __builtin_amdgcn_iglp_opt(1);
     step(qb, b * 2 * TE, b * 4 * VS, mask_tag);
   };
@@ -343,12 +327,8 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_b
   for (int s0 = 0; s0 < S - 1; ++s0) issue_next();
   // Retire the K row loads (and the first tiles with them) here: otherwise
   // the compiler, which does not see the tile loads, keeps the K loads
-  // pending around the loop and waits for them on every iteration.  The K
-  // chunks parked in LDS are stored only now, so that their wait does not
-  // hold back the tile loads above (the two HBM round trips overlap).
+  // pending around the loop and waits for them on every iteration.
   wait_vmem_le<0>();
-#pragma unroll
-  for (int c = KR; c < NC; ++c) *reinterpret_cast<bf16x8*>(&sKf[((c - KR) * NW + w) * 512 + 8 * l]) = kf[c];
   const int qfull = (Lq / BQ) * BQ;
   const int qdiag = CAUSAL ? min(k0 + BN, Lq) : qstart;  // [qstart, qdiag): tiles crossing the diagonal
   run(qstart, qdiag, std::true_type{});
@@ -754,11 +734,13 @@ static int launch_bwd(const T* q, const T* k, const T* v, const T* o, const floa
     hipLaunchKernelGGL((attn_bwd_dq_pipe_kernel<D, CAUSAL>), dim3((unsigned)(nqp * BH)), dim3(256), 0, st, q, k, v, o,
                        dout, lse, l2, delta, dq, (int)Lq, (int)Lk, (int)BH, (int)nqp, gp, sl2, scale);
     TT_LAUNCHED("attention backward dQ launch", st);
-    if constexpr (D == 128)
+    if constexpr (D == 128) {
       return launch_dkdv_w64(q, k, v, dout, l2, delta, dk, dv, BH, Lq, Lk, sl2, scale, CAUSAL, st);
-    hipLaunchKernelGGL((attn_bwd_dkdv_bf16_kernel<D, CAUSAL>), dim3((unsigned)(nkt * BH)), dim3(64 * NW), 0, st, q,
-                       k, v, dout, l2, delta, dk, dv, (int)Lq, (int)Lk, (int)BH, (int)nkt, gk, sl2, scale);
-    TT_LAUNCHED("attention backward dK/dV launch", st);
+    } else {
+      hipLaunchKernelGGL((attn_bwd_dkdv_bf16_kernel<D, CAUSAL>), dim3((unsigned)(nkt * BH)), dim3(64 * NW), 0, st,
+                         q, k, v, dout, l2, delta, dk, dv, (int)Lq, (int)Lk, (int)BH, (int)nkt, gk, sl2, scale);
+      TT_LAUNCHED("attention backward dK/dV launch", st);
+    }
   } else {
     constexpr int TPR = D / (16 / (int)sizeof(T));
     const int64_t dblk = (rows + (256 / TPR) - 1) / (256 / TPR);

@@ -73,9 +73,9 @@ __device__ __forceinline__ void agpr_drain(f32x16 (&a)[2][4], f32x16 (&b)[2][4])
 }
 
 constexpr int DKW_BN = 256, DKW_BQ = 32, DKW_STAGES = 4;
-#ifndef DKW_READ_AHEAD
-#define DKW_READ_AHEAD 4
-#endif
+// LDS reads run this many slots ahead of their MFMA (6 and 8 measured the
+// same as 4; whole dP slot pairs, so the carried operands are whole chunks).
+constexpr int DKW_READ_AHEAD = 4;
 static_assert(DKW_READ_AHEAD % 2 == 0 && DKW_READ_AHEAD >= 2 && DKW_READ_AHEAD <= 12, "read-ahead in whole dP slot pairs");
 
 // Bytes of the kernel's LDS block: Q and dO rings, LSE / -D rows, V rows.
