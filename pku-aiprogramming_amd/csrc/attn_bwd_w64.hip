@@ -25,7 +25,10 @@
 //   slots 32-47  MFMA S_{n+1} = Q_{n+1} K^T    (into the registers S_n and dP_n no longer need)
 //   slots 48-63  MFMA dK^T += Q_n^T dS_n       VALU half of P_{n+1}
 // with every LDS read issued a few slots ahead of its MFMA and a scheduling
-// barrier closing each slot.  Tile n is read until the end of iteration n, so
+// barrier closing each slot.  In the causal diagonal tiles a wave skips the
+// MFMAs of a key half that lies wholly after the tile's queries (in the first
+// four tiles of a 256-key block every wave's second half; 6 % of the kernel's
+// MFMAs at L = 4096, 1 % of its time).  Tile n is read until the end of iteration n, so
 // the tile issued after barrier n + 1 (tile n + 3) goes into the buffer of
 // tile n - 1: a 4-deep ring.  On the MI355X this runs at 72 % MFMA-busy
 // cycles for long non-causal heads against 62 % for the two-waves-per-SIMD
@@ -289,6 +292,16 @@ __device__ __forceinline__ void dkdv_w64_item(
       VV[1][c] = vvc[1][c];
     }
     bf16x8 pb[2][2], db[2][2];
+    // Under the causal mask a key half can lie wholly after a diagonal tile's
+    // queries (every P = 0): its MFMAs are skipped (a wave-uniform branch),
+    // those of tile n (dP, dV, dK) by live(h) and those of tile n + 1 (S) by
+    // live1(h).  A skipped half's scores and dP hold stale values that the
+    // mask zeroes or nothing reads.
+    const int klo = k0 + 32 * w;
+    auto live = [&](int h) __attribute__((always_inline)) { return !MASK || !CAUSAL || qb + BQ - 1 >= klo + 128 * h; };
+    auto live1 = [&](int h) __attribute__((always_inline)) {
+      return !MASK || !CAUSAL || qb + 2 * BQ - 1 >= klo + 128 * h;
+    };
     f32x4 lan[4];  // LSE rows of tile n + 1
     f32x16 ndn;    // -D rows of tile n + 1
     float prod[2];
@@ -381,16 +394,16 @@ __device__ __forceinline__ void dkdv_w64_item(
       // MFMA
       if constexpr (k < 16) {
         constexpr int c = k / 2, h = k % 2;
-        dp[h] = mfma_bf16_32x32x16(DA[c], VV[h][c], c == 0 ? nd : dp[h]);
+        if (live(h)) dp[h] = mfma_bf16_32x32x16(DA[c], VV[h][c], c == 0 ? nd : dp[h]);
       } else if constexpr (k < 32) {
         constexpr int i = (k - 16) / 2, h = k % 2;
-        mfma_acc_agpr(adv[h][i % ND], OV[i], pb[h][i / ND]);
+        if (live(h)) mfma_acc_agpr(adv[h][i % ND], OV[i], pb[h][i / ND]);
       } else if constexpr (k < 48) {
         constexpr int c = (k - 32) / 2, h = k % 2;
-        s[h] = mfma_bf16_32x32x16(QA[c], kf[h][c], c == 0 ? f32x16{} : s[h]);
+        if (live1(h)) s[h] = mfma_bf16_32x32x16(QA[c], kf[h][c], c == 0 ? f32x16{} : s[h]);
       } else {
         constexpr int i = (k - 48) / 2, h = k % 2;
-        mfma_acc_agpr(adk[h][i % ND], OQ[i], db[h][i / ND]);
+        if (live(h)) mfma_acc_agpr(adk[h][i % ND], OQ[i], db[h][i / ND]);
       }
       __builtin_amdgcn_sched_barrier(0);
     };

@@ -329,6 +329,7 @@ SHAPES = [
     (2, 1, 257, 513, 128, False),   # last key block holds one key
     (1, 1, 96, 40, 128, False),     # fewer keys than one wave's first half
     (1, 1, 544, 544, 128, True),    # a last key block of exactly one 32-key half
+    (1, 1, 1000, 1000, 128, True),  # four key blocks, each with its diagonal tiles, the last one ragged
 ]
 
 
