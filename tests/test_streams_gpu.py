@@ -3,7 +3,8 @@
 * two host threads, each with its own caller stream (default priority),
   running attention backward calls of different shapes at the same time:
   every result matches the float64 oracle (the per-stream workspaces keep
-  their -D / LSE buffers apart);
+  their -D / LSE buffers apart), also with two persistent d = 128 dK/dV
+  launches sharing the CUs;
 * one stream shared by two threads: the workspace lease keeps each call's
   launches together, so both threads' results stay correct;
 * allocation-failure injection (TT_FAIL_ALLOC_AFTER) in a child process:
@@ -87,6 +88,20 @@ def test_two_threads_two_streams_backward(capi):
     cases = [_case(1, 2, 4, 384, 128, True), _case(2, 1, 6, 256, 64, True)]
     streams = [capi.Stream(), capi.Stream()]
     _say("two threads, two streams: bf16 causal bwd [2,4,384,128] and [1,6,256,64], 4 reps each")
+    try:
+        _threads(capi, [s.handle for s in streams], cases, reps=4)
+    finally:
+        for s in streams:
+            s.destroy()
+
+
+def test_two_threads_two_streams_persistent_d128(capi):
+    # both calls run the persistent d = 128 dK/dV launch (one workgroup per CU
+    # at most): launches on the two streams share the CUs and must not wait
+    # for each other
+    cases = [_case(5, 2, 4, 384, 128, True), _case(6, 1, 8, 640, 128, True)]
+    streams = [capi.Stream(), capi.Stream()]
+    _say("two threads, two streams: bf16 causal bwd [2,4,384,128] and [1,8,640,128], 4 reps each")
     try:
         _threads(capi, [s.handle for s in streams], cases, reps=4)
     finally:
