@@ -11,8 +11,8 @@
 // Workgroup = 4 waves, one per SIMD (one workgroup per CU), 256 keys.  Wave w
 // owns two halves of 32 keys (lane = key) at k0 + 32 w and k0 + 128 + 32 w, so
 // every Q / dO operand it reads from LDS feeds one MFMA per half: a tile of
-// 32 queries costs a wave 64 MFMAs against 50 KB of LDS reads (half the LDS
-// traffic per MFMA of a 32-key wave).  The dK / dV accumulators (256
+// 32 queries costs a wave 64 MFMAs against 48 KB of operand reads from LDS
+// (0.75 KB per MFMA, against 1.25 KB for a wave of 32 keys).  The dK / dV accumulators (256
 // registers) live in the accumulation registers (AGPRs) of the 512-register
 // file a lone wave owns; K rows, scores and operands live in the 256
 // architectural VGPRs.  V rows sit in LDS; Q / dO tiles with their LSE and -D
@@ -27,7 +27,7 @@
 // with every LDS read issued a few slots ahead of its MFMA and a scheduling
 // barrier closing each slot.  In the causal diagonal tiles a wave skips the
 // MFMAs of a key half that lies wholly after the tile's queries (in the first
-// four tiles of a 256-key block every wave's second half; 6 % of the kernel's
+// four tiles of a 256-key block every wave's second half; 5 % of the kernel's
 // MFMAs at L = 4096, 1 % of its time).  Tile n is read until the end of iteration n, so
 // the tile issued after barrier n + 1 (tile n + 3) goes into the buffer of
 // tile n - 1: a 4-deep ring.  On the MI355X this runs at 72 % MFMA-busy
