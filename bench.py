@@ -624,10 +624,11 @@ def main(argv=None):
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--only", choices=["all", "fwdbwd", "configs", "decode", "copy", "ceiling", "softmax", "gemm", "io",
-                                       "sustain"],
+                                       "sustain", "seqsweep"],
                     default="all",
                     help="run one workload only (for profiler runs; 'copy' is the 1 GiB calibration copy, "
-                         "'ceiling' the library bf16 GEMM reference, 'sustain' the --sustain loop)")
+                         "'ceiling' the library bf16 GEMM reference, 'sustain' the --sustain loop, 'seqsweep' "
+                         "the c5 step at L = 1024 .. 16384 over the same number of tokens)")
     ap.add_argument("--sustain", default="3:all:8", metavar="CID:PART:SECONDS",
                     help="with --only sustain: config (1, 2, 3 or 5), part (all, fwd or bwd) and duration of a "
                          "loop of 200-step batches")
@@ -660,6 +661,20 @@ def main(argv=None):
             ap.error("--sustain part must be all, fwd or bwd")
         print(json.dumps({"metric": "ms per step over a sustained loop", "config": f"c{cid}", "part": part,
                           **run_sustain(T, cfg, part, float(secs))}), flush=True)
+        return 0
+
+    if args.only == "seqsweep":
+        # the c5 step (causal, bf16, H = 32, d = 128) at other sequence lengths, B * L = 16384 tokens
+        cases = []
+        for i, L in enumerate((1024, 2048, 4096, 8192, 16384)):
+            cfg = GpuConfig(50 + i, (C5["B"] * C5["L"]) // L, C5["H"], L, L, C5["d"], "bf16", True, True)
+            ms = run_config(T, cfg, args.steps, args.warmup)
+            tf = config_flops(cfg) / (ms * 1e-3) / 1e12
+            cases.append({"workload": f"causal fwd+bwd bf16 B={cfg.B} H={cfg.H} L={L} d={cfg.d}", "ms": ms,
+                          "value": tf, "unit": "TFLOP/s", "frac_of_peak": tf / PEAK_BF16_TFLOPS})
+            print(f"seqsweep L={L}: {ms:.4f} ms, {tf:.1f} TFLOP/s", file=sys.stderr, flush=True)
+        print(json.dumps({"metric": "attn fwd+bwd TFLOP/s by sequence length (same tokens per step)",
+                          "steps": args.steps, "warmup": args.warmup, "cases": cases}), flush=True)
         return 0
 
     out = {
