@@ -39,11 +39,27 @@
 // compiler otherwise gives every MFMA of a kernel with more than 256 registers
 // an AGPR destination, and the scores would then need 64 more AGPRs than the
 // file has.  This file is built with -mllvm -amdgpu-mfma-vgpr-form=1 so the
-// builtin MFMAs (S, dP) write VGPRs.  The compiler does not know the asm
-// MFMAs' hazards, so the asm carries its own wait states: 2 before each MFMA
-// (a VALU write of an MFMA source needs 2; the schedule also keeps every such
-// write at least one slot ahead) and 3 x 8 after the last one before the
-// accumulators are read (an MFMA of 8 passes needs 11).
+// builtin MFMAs (S, dP) write VGPRs.  The compiler's hazard recognizer does
+// not look inside inline asm, so the asm carries its own wait states, sized by
+// the CDNA4 ISA reference guide, chapter "Matrix Arithmetic Instructions",
+// table "Dependency Resolution: Required Independent Instructions" (the same
+// counts as LLVM's GCNHazardRecognizer for gfx950, checkMAIHazards90A and
+// checkMAIVALUHazards):
+//   * "VALU write VGPR -> MFMA read of that VGPR (SrcA/B/C)": 2 wait states.
+//     Each asm MFMA's P / dS operand (SrcB) comes from VALU conversions, and
+//     its first SrcC from the v_accvgpr_write that zeroes the accumulator:
+//     the "s_nop 1" (2 wait states) in mfma_acc_agpr covers it whatever the
+//     schedule; the slot schedule also keeps every such write at least one
+//     MFMA slot ahead.
+//   * "XDL write VGPR/AGPR -> VALU read, VMEM / LDS read or export of it":
+//     passes + 3 wait states, one more on gfx950 for XDL ops of more than two
+//     passes; v_mfma_f32_32x32x16_bf16 is 8 passes (32 cycles), so 11 or 12.
+//     agpr_drain gives 3 x "s_nop 7" = 24 before the epilogue's first
+//     v_accvgpr_read of an accumulator.
+//   * "XDL write -> XDL read as SrcC of the same registers, same opcode,
+//     back to back" (the dK / dV accumulation chains): no wait states.
+// The operands the asm reads from LDS (SrcA) need a data wait, not a wait
+// state: the compiler's s_waitcnt insertion does see inline-asm operands.
 #include <hip/hip_runtime.h>
 
 #include <type_traits>
@@ -55,7 +71,8 @@ namespace tt {
 
 namespace {
 
-// acc += a b on the matrix core, acc in AGPRs (see the file comment).
+// acc += a b on the matrix core, acc in AGPRs.  "s_nop 1": the 2 wait states
+// of the rule "VALU write VGPR -> MFMA read" (file comment).
 __device__ __forceinline__ void mfma_acc_agpr(f32x16& acc, const bf16x8& a, const bf16x8& b) {
   asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
 }
@@ -67,7 +84,9 @@ __device__ __forceinline__ void pin(T& x) {
   asm volatile("" : "+v"(x));
 }
 
-// Wait states between the last asm MFMA and the first read of its result.
+// Wait states between the last asm MFMA and the first read of its result:
+// 24, against the 11 (12 on gfx950) of the rule "XDL write -> VALU read" for
+// an 8-pass MFMA (file comment).
 __device__ __forceinline__ void agpr_drain(f32x16 (&a)[2][4], f32x16 (&b)[2][4]) {
   asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7"
                : "+a"(a[0][0]), "+a"(a[0][1]), "+a"(a[0][2]), "+a"(a[0][3]), "+a"(a[1][0]), "+a"(a[1][1]),
@@ -237,6 +256,10 @@ __device__ __forceinline__ void dkdv_w64_item(
   f32x4 la[2];  // LSE log2(e) rows j = 2, 3 of the current tile (registers r = 8..15)
   constexpr int A = DKW_READ_AHEAD;  // LDS reads run A slots ahead of their MFMA
   constexpr int KB = 32 - A;         // slot of barrier n + 1 (before the first read of tile n + 1)
+  // Tile n + 3's PER loads go at slots KB + 5, KB + 11, ...: all of them must
+  // fall inside the 64 slots, or barrier_next's constant vmcnt would count a
+  // load that was never issued.
+  static_assert(KB + 5 + 6 * (PER - 1) <= 63, "tile loads past the last slot of an iteration");
   bf16x8 dac[A / 2], vvc[2][A / 2];  // operands of the current tile's first dP slots, read ahead
 
   // Barrier n + 1: this wave's loads of tile n + 1 have landed (loads retire

@@ -12,6 +12,8 @@
 //     int  alloc(size_t bytes, void** p);  // TT_OK or an error code; *p set on success
 //     void release(void* p);               // return a block to the device
 //     int  sync(void* stream);             // wait for all work queued on `stream`
+//     int  order_after_library(void* stream);  // work queued on `stream` from now on
+//                                              // waits for the library stream's queued work
 //   };
 //
 // so that the same code is compiled into the HIP runtime and, with a fake
@@ -154,7 +156,10 @@ class BlockCache {
 // calls on one stream from several host threads cannot interleave their
 // launches; the stream then orders the kernels of consecutive calls.  A
 // buffer that must grow is replaced only after the stream that used it has
-// drained (its last kernels may still read it).
+// drained (its last kernels may still read it).  A buffer handed to a stream
+// for the first time is a block of the BlockCache, which tt_free may have
+// returned while work on the library stream still used it: that stream is
+// first ordered after the library stream's queued work.
 template <class Backend>
 class WorkspaceCache {
  public:
@@ -233,7 +238,11 @@ class WorkspaceCache {
       s = Slot{};
     }
     void* p = nullptr;
-    const int rc = blocks_.alloc(bytes, &p);
+    int rc = blocks_.alloc(bytes, &p);
+    if (!rc) {
+      rc = be_.order_after_library(stream);
+      if (rc) blocks_.release(p);
+    }
     if (rc) {
       slots_.erase({stream, user});
       return rc;

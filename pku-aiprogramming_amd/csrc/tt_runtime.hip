@@ -81,6 +81,20 @@ struct HipBackend {
     const hipError_t e = hipStreamSynchronize(static_cast<hipStream_t>(stream));
     return e == hipSuccess ? TT_OK : hip_fail(e, "hipStreamSynchronize (workspace)");
   }
+  // A block tt_free returned while library-stream work still used it may
+  // become another stream's workspace: that stream waits for the library
+  // stream's queued work (an event, no host wait).  Called under the
+  // workspace lock, which also guards `order_ev`.
+  hipEvent_t order_ev = nullptr;
+  int order_after_library(void* stream) {
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (!s || s == g_stream) return TT_OK;
+    hipError_t e = hipSuccess;
+    if (!order_ev) e = hipEventCreateWithFlags(&order_ev, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventRecord(order_ev, g_stream);
+    if (e == hipSuccess) e = hipStreamWaitEvent(s, order_ev, 0);
+    return e == hipSuccess ? TT_OK : hip_fail(e, "ordering a new workspace after the library stream");
+  }
 };
 static HipBackend g_backend;
 static BlockCache<HipBackend> g_blocks(g_backend);

@@ -82,6 +82,15 @@ class Tensor(Value):
             raise TypeError(f"Tensor.data: dtype {value.dtype} does not match {self.dtype}")
         self.cached_data = value.realize_cached_data()
 
+    @classmethod
+    def make_const(cls, data, requires_grad: bool = False) -> "Tensor":
+        """A leaf holding `data` (a Tensor argument gives its realised data,
+        not the Tensor itself), as the reference's Tensor.make_const
+        (operators.py:70-79)."""
+        if isinstance(data, Tensor):
+            data = data.realize_cached_data()
+        return super().make_const(data, requires_grad=requires_grad)
+
     def detach(self) -> "Tensor":
         return Tensor.make_const(self.realize_cached_data())
 

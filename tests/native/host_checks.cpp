@@ -28,7 +28,8 @@ static int g_failures = 0;
 
 struct FakeBackend {
   AllocFailureInjector inject;
-  std::atomic<long> allocs{0}, releases{0}, syncs{0};
+  std::atomic<long> allocs{0}, releases{0}, syncs{0}, orders{0};
+  std::atomic<void*> last_ordered{nullptr};
   int alloc(size_t bytes, void** p) {
     if (inject.next_fails()) return 4;
     *p = std::malloc(bytes);
@@ -41,6 +42,11 @@ struct FakeBackend {
   }
   int sync(void*) {
     ++syncs;
+    return 0;
+  }
+  int order_after_library(void* stream) {
+    ++orders;
+    last_ordered = stream;
     return 0;
   }
 };
@@ -89,17 +95,38 @@ static void workspace_checks() {
   {
     WorkspaceCache<FakeBackend>::Lease l(ws);
     CHECK(l.get(&s1, 0, 100, &p) == 0);
-    CHECK(l.get(&s1, 0, 64, &q) == 0 && q == p);  // fits: same buffer, no sync
+    // a new buffer: its stream is ordered after the library stream first
+    CHECK(be.orders == 1 && be.last_ordered == (void*)&s1);
+    CHECK(l.get(&s1, 0, 64, &q) == 0 && q == p);  // fits: same buffer, no sync, no new ordering
+    CHECK(be.orders == 1);
     CHECK(l.get(&s2, 0, 64, &r) == 0 && r != p);  // another stream: its own buffer
+    CHECK(be.orders == 2 && be.last_ordered == (void*)&s2);
   }
   CHECK(be.syncs == 0 && ws.count() == 2);
+  // A block freed while library-stream work may still use it (tt_free does
+  // not wait) and handed to another stream as its workspace: the ordering
+  // step comes before the buffer is returned.
+  {
+    void* freed = nullptr;
+    CHECK(bc.alloc(4096, &freed) == 0);
+    CHECK(bc.release(freed));
+    int s3 = 0;
+    {
+      WorkspaceCache<FakeBackend>::Lease l(ws);
+      void* w3 = nullptr;
+      const long before = be.orders;
+      CHECK(l.get(&s3, 0, 4000, &w3) == 0 && w3 == freed);
+      CHECK(be.orders == before + 1 && be.last_ordered == (void*)&s3);
+    }
+    CHECK(ws.release_stream(&s3) == 0);
+  }
   {
     WorkspaceCache<FakeBackend>::Lease l(ws);
     void* big = nullptr;
     CHECK(l.get(&s1, 0, 1 << 21, &big) == 0);  // grows: waits for stream 1 first
     std::memset(big, 3, 1 << 21);
   }
-  CHECK(be.syncs == 1 && ws.bytes_held() == (size_t(1) << 21) + 64);
+  CHECK(be.syncs == 2 && ws.bytes_held() == (size_t(1) << 21) + 64);  // (the first sync: release_stream(&s3))
   // a failed growth leaves no slot behind and reports the error
   be.inject.set_limit(0);
   {

@@ -258,6 +258,39 @@ def test_long_sequence_few_heads_bf16(capi):
     _check("head 1 dV", dv[:, 1:2], rv, TOL["bf16"])
 
 
+PERSISTENT_SCHEDULES = [
+    # (B, H, L): the d = 128 dK/dV kernel runs one workgroup per CU (256 on the
+    # MI355X) over (256-key block, head) items.
+    # 12 heads x 32 key blocks = 384 items; B*H % 8 != 0, so the items are
+    # dealt over all workgroups without the per-XCD head grouping, in two
+    # rounds, the second one ragged (128 items for 256 workgroups).
+    (1, 12, 8192),
+    # 24 heads x 16 key blocks = 384 items; B*H % 8 == 0, so each XCD owns 3
+    # heads (48 items for its 32 workgroups): one full round and a ragged one.
+    (3, 8, 4096),
+]
+
+
+@pytest.mark.parametrize("B,H,L", PERSISTENT_SCHEDULES)
+def test_persistent_dkdv_schedules_bf16(capi, B, H, L):
+    """The two regimes of the persistent dK/dV schedule that c5 (2048 items,
+    eight full rounds with per-XCD head grouping) does not reach: every head
+    against the fp32 kernels and through the identities, one head against the
+    float64 oracle."""
+    d = 128
+    _say(f"persistent dK/dV schedule: bf16 causal B={B} H={H} L={L} d={d}")
+    rng = np.random.default_rng(1000 * H + B)
+    x = {n: orc.bf16_round(rng.standard_normal((B, H, L, d), dtype=np.float32)) for n in ("q", "k", "v", "do")}
+    scale = float(np.float32(1.0 / math.sqrt(d)))
+    b = _run_fwd(capi, x, "bf16", scale, True)
+    o, lse = b["o"].download(), b["lse"].download()
+    dq, dk, dv = _run_bwd(capi, b, x["do"], "bf16", scale, True)
+    _identities("sched", x, o, lse, dq, dk, dv, scale, True, TOL["bf16"])
+    _all_heads_vs_f32(capi, "sched", x, o, lse, dq, dk, dv, scale, True, TOL["bf16"])
+    bb, hh = B - 1, H - 1  # the last head: its items come last in both schedules
+    _sampled_heads("sched", x, o, lse, dq, dk, dv, scale, True, [(bb, hh)], TOL["bf16"])
+
+
 DECODE_LONG_SPLITS = [
     # (B, H, Lkv, d): 512 heads -> five 2048-key splits per head, the last one
     # partial (808 keys), merged by the combine kernel

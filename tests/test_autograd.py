@@ -199,6 +199,46 @@ def test_device_handle(ops):
     assert device.cpu() == device.cpu() and hash(device.cpu()) == hash(device.Device("cpu"))
     assert repr(device.cpu()) == "cpu()" and device.cpu().enabled()
     assert device.Device("gpu") != device.cpu()
+    # the rest of the reference's device module (device.py:9-59)
+    assert isinstance(device.cpu(), device.CPUDevice) and isinstance(device.cpu(), device.Device)
+    assert device.CPUDevice() == device.cpu() and {device.cpu(): 1}[device.CPUDevice()] == 1
+    assert device.default_device() == device.cpu() and device.all_devices() == [device.cpu()]
+
+
+def test_cpu_device_factories(ops):
+    import device
+
+    c = device.cpu()
+    z = c.zeros(2, 3)
+    assert z.shape == (2, 3) and z.dtype == np.float32 and not z.any()
+    o = c.ones(4, dtype="float64")
+    assert o.dtype == np.float64 and (o == 1).all()
+    np.random.seed(5)
+    r = c.randn(3, 2)
+    np.random.seed(5)
+    assert r.shape == (3, 2) and np.array_equal(r, np.random.standard_normal((3, 2)))
+    np.random.seed(6)
+    u = c.rand(5)
+    np.random.seed(6)
+    assert np.array_equal(u, np.random.random_sample(5)) and ((u >= 0) & (u < 1)).all()
+    h = c.one_hot(4, np.array([2, 0]))
+    np.testing.assert_array_equal(h, [[0, 0, 1, 0], [1, 0, 0, 0]])
+    assert h.dtype == np.float32
+    assert c.empty((2, 2)).shape == (2, 2) and c.empty((1,), dtype="int32").dtype == np.int32
+    f = c.full((2, 1), 7.5)
+    assert f.dtype == np.float32 and (f == 7.5).all()
+
+
+def test_make_const_unwraps_a_tensor_and_takes_requires_grad_positionally(ops):
+    a = ops.Tensor(np.arange(3.0))
+    c = ops.Tensor.make_const(a)
+    assert isinstance(c.cached_data, np.ndarray) and c.numpy() is a.numpy()
+    assert c.is_leaf() and not c.requires_grad
+    g = ops.Tensor.make_const(np.ones(2), True)
+    assert g.requires_grad and isinstance(g, ops.Tensor)
+    y = ops.summation(g * 3.0)
+    y.backward()
+    np.testing.assert_array_equal(g.grad.numpy(), [3.0, 3.0])
 
 
 def test_causal_mask_closed_form(ops):

@@ -1,9 +1,10 @@
 """GPU test of the allocation-free backward entry point
-(tt_attn_bwd_bf16_noalloc) through the C-ABI: two calls in a row, the
-second with a smaller input, each against tt_attn_bwd_bf16 on the same
-inputs (the same kernels, so the results must agree bit for bit), with the
-library allocator's statistics unchanged by the calls; sizes beyond the
-static scratch are refused before any launch.
+(tt_attn_bwd_bf16_noalloc) through the C-ABI: calls in a row, each with a
+smaller input than the one before, each against tt_attn_bwd_bf16 on the
+same inputs (the same kernels, so the results must agree bit for bit) and
+against the float64 oracle, with the library allocator's statistics
+unchanged by the calls; sizes beyond the static scratch are refused before
+any launch.
 """
 import ctypes as C
 import math
@@ -47,7 +48,12 @@ def _stats(capi):
 
 @pytest.mark.parametrize("order", ["large_then_small"])
 def test_noalloc_backward_matches_the_allocating_entry_point(capi, order):
-    cases = [(11, 2, 4, 512, 128, True), (12, 1, 3, 200, 64, False)]  # second call smaller
+    # each call smaller than the one before (B*H*L rows: 4096, 2304, 1200,
+    # 600, 260), covering d = 128 and d = 64 (the dQ kernel writes the rows
+    # into the static scratch) and d = 32 (a separate row pre-pass kernel
+    # writes them), causal and not
+    cases = [(11, 2, 4, 512, 128, True), (13, 2, 3, 384, 64, True), (14, 1, 4, 300, 32, True),
+             (12, 1, 3, 200, 64, False), (15, 1, 2, 130, 32, False)]
     for seed, B, H, L, d, causal in cases:
         print(f"noalloc bwd B={B} H={H} L={L} d={d} causal={causal}", flush=True)
         scale = float(np.float32(1 / math.sqrt(d)))
