@@ -385,8 +385,8 @@ def run_copy(T, steps, warmup, nbytes=1 << 30):
 # algorithmic bytes = rows * cols * 4 read + the same written.
 SOFTMAX_CASES = [
     dict(name="rows 262144 x 1024 (one wave per row)", rows=262144, cols=1024),
-    dict(name="rows 4096 x 65536 (16 waves per row)", rows=4096, cols=65536),
-    dict(name="rows 1024 x 262144 (two-pass stream)", rows=1024, cols=262144),
+    dict(name="rows 4096 x 65536 (8 workgroups per row, partials exchanged)", rows=4096, cols=65536),
+    dict(name="rows 1024 x 262144 (16 workgroups per row, partials exchanged)", rows=1024, cols=262144),
 ]
 
 

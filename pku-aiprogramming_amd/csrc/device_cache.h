@@ -166,6 +166,7 @@ class WorkspaceCache {
   struct Slot {
     void* ptr = nullptr;
     size_t bytes = 0;
+    uint64_t uses = 0;  // earlier get() calls that returned this buffer
   };
 
   WorkspaceCache(Backend& be, BlockCache<Backend>& blocks) : be_(be), blocks_(blocks) {}
@@ -175,7 +176,11 @@ class WorkspaceCache {
     explicit Lease(WorkspaceCache& c) : c_(c), lk_(c.mu_) {}
     // A buffer of at least `bytes` for `user` on `stream`, valid while the
     // lease lives (and for the device work queued on `stream` meanwhile).
-    int get(void* stream, int user, size_t bytes, void** ptr) { return c_.get_locked(stream, user, bytes, ptr); }
+    // *uses (optional): how many earlier get() calls returned this same
+    // buffer; 0 for a new buffer, whose contents are undefined.
+    int get(void* stream, int user, size_t bytes, void** ptr, uint64_t* uses = nullptr) {
+      return c_.get_locked(stream, user, bytes, ptr, uses);
+    }
 
    private:
     WorkspaceCache& c_;
@@ -225,10 +230,12 @@ class WorkspaceCache {
   }
 
  private:
-  int get_locked(void* stream, int user, size_t bytes, void** ptr) {
+  int get_locked(void* stream, int user, size_t bytes, void** ptr, uint64_t* uses) {
     Slot& s = slots_[{stream, user}];
     if (s.ptr && bytes <= s.bytes) {
       *ptr = s.ptr;
+      if (uses) *uses = s.uses;
+      ++s.uses;
       return 0;
     }
     if (s.ptr) {
@@ -249,7 +256,9 @@ class WorkspaceCache {
     }
     s.ptr = p;
     s.bytes = bytes;
+    s.uses = 1;
     *ptr = p;
+    if (uses) *uses = 0;
     return 0;
   }
 

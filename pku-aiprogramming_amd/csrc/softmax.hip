@@ -9,14 +9,19 @@
 //   m = max_c x[c];  e[c] = exp(x[c] - m);  s = sum_c e[c];  y[c] = e[c] / s
 // (the sum's association order differs: lanes, then a butterfly).
 //
-// Three shapes of work, all coalesced (lane t of a row group reads columns
+// Shapes of work, all coalesced (lane t of a row group reads columns
 // t, t + G, t + 2G, ... for group width G):
 //   cols <= 64:   G = the next power of two >= cols lanes per row, 64 / G
 //                 rows per wave, one element per lane;
 //   cols <= 2048: one wave per row, up to 32 elements per lane in registers;
-//   cols <= 65536: one workgroup of 4 or 16 waves per row, up to 64
-//                 elements per lane in registers, partials through LDS;
-//   longer rows:  one workgroup of 16 waves per row; pass 1 keeps a running
+//   cols <= 8192 (and longer rows that are not 16-byte aligned, up to 65536):
+//                 one workgroup of 4 or 16 waves per row, up to 64 elements
+//                 per lane in registers, partials through LDS;
+//   longer aligned rows, up to 2 M columns: the row is split over up to 64
+//                 workgroups that each hold their chunk in registers and
+//                 exchange (max, sum) partials through device memory (one
+//                 HBM read and one write per element);
+//   the rest:     one workgroup of 16 waves per row; pass 1 keeps a running
 //                 (max, sum) per lane, pass 2 rereads the row and writes it.
 #include <hip/hip_runtime.h>
 
@@ -216,6 +221,118 @@ __global__ __launch_bounds__(64 * W) void k_softmax_stream(const float* __restri
   }
 }
 
+// Rows split over workgroups.  Workgroup id = row * nchunk + chunk holds
+// columns [chunk * CW, chunk * CW + CW) of its row in registers (lane t: the
+// 16-byte vectors at 4 t + 1024 k, k < NE4), forms the chunk's max m_c and
+// sum s_c of exp(x - m_c), and publishes them as two 64-bit words
+// (generation << 32 | float bits) in `slots` (two words per chunk, row
+// major).  It then waits until every chunk of its row has published under
+// the current generation, merges the partials into the row's (M, S) and
+// writes y = exp(x - m_c) * (exp(m_c - M) / S): one read and one write of
+// each element.  The generation is new for every launch on a slot buffer
+// (the host counts the buffer's uses and zero-fills a new one), so words of
+// earlier launches never match.  Each word is one relaxed agent-scope
+// atomic (coherent across the XCDs' L2s); no other data crosses workgroups,
+// so no fence is needed.
+//
+// The wait cannot deadlock: workgroups are dispatched in id order, so every
+// row below the one at the dispatch front has all of its (at most 64)
+// chunks resident or done, finishes, and frees slots for the front row.  It
+// is bounded all the same: after about 2^20 polls a workgroup stops waiting
+// and writes NaN for its chunk.  A workgroup writes only the chunk it has
+// already read, so x == y (in place) is fine.
+constexpr int kSplitMaxChunks = 64;
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+
+template <int NE4>
+__global__ __launch_bounds__(kBlock) void k_softmax_split(const float* x, float* y, int64_t cols, int nchunk,
+                                                         unsigned long long* slots, unsigned gen) {
+  constexpr int CW = 1024 * NE4;  // columns per chunk
+  __shared__ float red_m[4], red_s[4];
+  const int t = threadIdx.x, w = t >> 6, l = t & 63;
+  const int64_t row = (int64_t)blockIdx.x / nchunk;
+  const int chunk = (int)((int64_t)blockIdx.x - row * nchunk);
+  const int64_t c0 = (int64_t)chunk * CW;
+  const int64_t rem = cols - c0;  // > 0; columns of the row from this chunk on
+  const float* xr = x + row * cols + c0;
+  float* yr = y + row * cols + c0;
+  f32x4v v[NE4];
+#pragma unroll
+  for (int k = 0; k < NE4; ++k) {
+    const int c = 4 * t + 1024 * k;  // cols % 4 == 0: a vector is wholly inside or outside the row
+    v[k] = c < rem ? __builtin_nontemporal_load(reinterpret_cast<const f32x4v*>(xr + c))
+                   : f32x4v{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+  }
+  float m = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < NE4; ++k) m = fmaxf(m, fmaxf(fmaxf(v[k].x, v[k].y), fmaxf(v[k].z, v[k].w)));
+  m = group_max<64>(m);
+  if (l == 0) red_m[w] = m;
+  __syncthreads();
+  m = fmaxf(fmaxf(red_m[0], red_m[1]), fmaxf(red_m[2], red_m[3]));
+  // a chunk with no finite value (m = -inf) has every exp 0 and s = 0
+  const float mb = m == -INFINITY ? 0.f : m;
+  float s = 0.f;
+#pragma unroll
+  for (int k = 0; k < NE4; ++k) {
+    v[k].x = ex(v[k].x - mb);
+    v[k].y = ex(v[k].y - mb);
+    v[k].z = ex(v[k].z - mb);
+    v[k].w = ex(v[k].w - mb);
+    s += (v[k].x + v[k].y) + (v[k].z + v[k].w);
+  }
+  s = group_sum<64>(s);
+  if (l == 0) red_s[w] = s;
+  __syncthreads();
+  s = (red_s[0] + red_s[1]) + (red_s[2] + red_s[3]);
+
+  unsigned long long* rs = slots + 2 * row * nchunk;
+  const unsigned long long tag = (unsigned long long)gen << 32;
+  if (t == 0) {
+    __hip_atomic_store(rs + 2 * chunk, tag | __float_as_uint(m), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(rs + 2 * chunk + 1, tag | __float_as_uint(s), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  // thread j < nchunk waits for chunk j's partial and merges it
+  float pm = -INFINITY, ps = 0.f;
+  bool ok = true;
+  if (t < nchunk) {
+    unsigned long long a = 0, b = 0;
+    for (int polls = 0;; ++polls) {
+      a = __hip_atomic_load(rs + 2 * t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      b = __hip_atomic_load(rs + 2 * t + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if ((unsigned)(a >> 32) == gen && (unsigned)(b >> 32) == gen) break;
+      if (polls >= (1 << 20)) {
+        ok = false;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(2);
+    }
+    pm = __uint_as_float((unsigned)a);
+    ps = __uint_as_float((unsigned)b);
+  }
+  // (M, S) over the workgroup's threads; pairs with s = 0 add nothing
+  float M = group_max<64>(pm);
+  float S = group_sum<64>(ps == 0.f ? 0.f : ps * ex(pm - M));
+  const int bad = __syncthreads_or(!ok);
+  if (l == 0) {
+    red_m[w] = M;
+    red_s[w] = S;
+  }
+  __syncthreads();
+  M = fmaxf(fmaxf(red_m[0], red_m[1]), fmaxf(red_m[2], red_m[3]));
+  S = 0.f;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) S += red_s[k] == 0.f ? 0.f : red_s[k] * ex(red_m[k] - M);
+  // exp(m - M) / S; a row with no finite value gives NaN (0 / 0 and
+  // -inf - -inf), as the reference's x - max does
+  const float f = bad ? NAN : (m == -INFINITY && M != -INFINITY ? 0.f : ex(m - M)) / S;
+#pragma unroll
+  for (int k = 0; k < NE4; ++k) {
+    const int c = 4 * t + 1024 * k;
+    if (c < rem) __builtin_nontemporal_store(v[k] * f, reinterpret_cast<f32x4v*>(yr + c));
+  }
+}
+
 int blocks_for(int64_t rows, int64_t rows_per_block) {
   const int64_t b = (rows + rows_per_block - 1) / rows_per_block;
   return (int)(b < 65536 ? b : 65536);  // grid-stride beyond this
@@ -235,6 +352,35 @@ extern "C" int tt_softmax_rows_f32(const float* x, float* y, int64_t rows, int64
   int rc = ensure_init();
   if (rc) return rc;
   hipStream_t s = stream_or_default(stream);
+  // Long 16-byte aligned rows: split over workgroups (k_softmax_split), with
+  // chunks of 4096 / 8192 / 16384 / 32768 columns for rows up to 16 Ki /
+  // 64 Ki / 256 Ki / 2 Mi columns (measured best on the MI355X for each).
+  const bool aligned = cols % 4 == 0 && ((uintptr_t)x % 16) == 0 && ((uintptr_t)y % 16) == 0;
+  if (aligned && cols > 8192 && cols <= int64_t(kSplitMaxChunks) * 32768) {
+    const int ne4 = cols <= 16384 ? 4 : cols <= 65536 ? 8 : cols <= 262144 ? 16 : 32;
+    const int64_t cw = 1024 * ne4, nchunk = (cols + cw - 1) / cw;
+    if (rows * nchunk <= 0x7fffffff) {
+      unsigned long long* slots = nullptr;
+      uint64_t uses = 0;
+      const size_t bytes = (size_t)(rows * nchunk) * 2 * sizeof(unsigned long long);
+      WorkspaceLease ws;  // held until the kernel that reads the slots is queued
+      if ((rc = ws.get(s, kWsSoftmaxPartials, bytes, (void**)&slots, &uses))) return rc;
+      const unsigned gen = (unsigned)(uses % 0xffffffffull) + 1;  // 1 .. 2^32 - 1
+      if (gen == 1 &&  // a new buffer (or a wrapped count): no word may hold a live generation
+          (rc = tt_elementwise(TT_EW_FILL, TT_F32, slots, nullptr, nullptr, (int64_t)(bytes / 4), 0.0, 0.0, 0, s)))
+        return rc;
+      const dim3 grid((unsigned)(rows * nchunk)), blk(kBlock);
+      const int n = (int)nchunk;
+      switch (ne4) {
+        case 4: hipLaunchKernelGGL(k_softmax_split<4>, grid, blk, 0, s, x, y, cols, n, slots, gen); break;
+        case 8: hipLaunchKernelGGL(k_softmax_split<8>, grid, blk, 0, s, x, y, cols, n, slots, gen); break;
+        case 16: hipLaunchKernelGGL(k_softmax_split<16>, grid, blk, 0, s, x, y, cols, n, slots, gen); break;
+        default: hipLaunchKernelGGL(k_softmax_split<32>, grid, blk, 0, s, x, y, cols, n, slots, gen); break;
+      }
+      TT_LAUNCHED("tt_softmax_rows_f32", s);
+      return ok();
+    }
+  }
   const int c = (int)cols;
 #define TT_SMALL(G)                                                                                 \
   hipLaunchKernelGGL(k_softmax_small<G>, dim3(blocks_for(rows, kBlock / G)), dim3(kBlock), 0, s, x, y, \

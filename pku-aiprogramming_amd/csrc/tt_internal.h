@@ -38,14 +38,16 @@ void* noalloc_scratch(size_t* bytes);
 // grown on demand and kept for reuse.  A lease holds the workspace lock from
 // get() until it is destroyed: keep it alive until every kernel that reads
 // the buffer has been launched on that stream.
-enum { kWsBackwardRows = 0, kWsDecodePartials = 1, kWsForwardSplits = 2 };
+enum { kWsBackwardRows = 0, kWsDecodePartials = 1, kWsForwardSplits = 2, kWsSoftmaxPartials = 3 };
 class WorkspaceLease {
  public:
   WorkspaceLease();
   ~WorkspaceLease();
   WorkspaceLease(const WorkspaceLease&) = delete;
   WorkspaceLease& operator=(const WorkspaceLease&) = delete;
-  int get(hipStream_t stream, int user, size_t bytes, void** ptr);
+  // *uses (optional): earlier get() calls that returned the same buffer (0:
+  // a new buffer with undefined contents).
+  int get(hipStream_t stream, int user, size_t bytes, void** ptr, uint64_t* uses = nullptr);
 
  private:
   struct Impl;

@@ -137,8 +137,8 @@ struct WorkspaceLease::Impl {
 };
 WorkspaceLease::WorkspaceLease() : impl_(new Impl) {}
 WorkspaceLease::~WorkspaceLease() { delete impl_; }
-int WorkspaceLease::get(hipStream_t s, int user, size_t bytes, void** ptr) {
-  return impl_->lease.get(static_cast<void*>(s), user, bytes, ptr);
+int WorkspaceLease::get(hipStream_t s, int user, size_t bytes, void** ptr, uint64_t* uses) {
+  return impl_->lease.get(static_cast<void*>(s), user, bytes, ptr, uses);
 }
 
 // ---------------------------------------------------------------- elementwise

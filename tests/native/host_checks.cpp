@@ -94,10 +94,12 @@ static void workspace_checks() {
   void *p = nullptr, *q = nullptr, *r = nullptr;
   {
     WorkspaceCache<FakeBackend>::Lease l(ws);
-    CHECK(l.get(&s1, 0, 100, &p) == 0);
+    uint64_t uses = 99;
+    CHECK(l.get(&s1, 0, 100, &p, &uses) == 0 && uses == 0);  // a new buffer: no earlier use
     // a new buffer: its stream is ordered after the library stream first
     CHECK(be.orders == 1 && be.last_ordered == (void*)&s1);
-    CHECK(l.get(&s1, 0, 64, &q) == 0 && q == p);  // fits: same buffer, no sync, no new ordering
+    CHECK(l.get(&s1, 0, 64, &q, &uses) == 0 && q == p && uses == 1);  // fits: same buffer, no sync, no new ordering
+    CHECK(l.get(&s1, 0, 100, &q, &uses) == 0 && q == p && uses == 2);
     CHECK(be.orders == 1);
     CHECK(l.get(&s2, 0, 64, &r) == 0 && r != p);  // another stream: its own buffer
     CHECK(be.orders == 2 && be.last_ordered == (void*)&s2);
@@ -123,7 +125,8 @@ static void workspace_checks() {
   {
     WorkspaceCache<FakeBackend>::Lease l(ws);
     void* big = nullptr;
-    CHECK(l.get(&s1, 0, 1 << 21, &big) == 0);  // grows: waits for stream 1 first
+    uint64_t uses = 99;
+    CHECK(l.get(&s1, 0, 1 << 21, &big, &uses) == 0 && uses == 0);  // grows: waits for stream 1 first; a new buffer
     std::memset(big, 3, 1 << 21);
   }
   CHECK(be.syncs == 2 && ws.bytes_held() == (size_t(1) << 21) + 64);  // (the first sync: release_stream(&s3))

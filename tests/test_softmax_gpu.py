@@ -51,8 +51,9 @@ def _check(name, y, x):
 
 
 # every kernel shape: lane groups of 1..64, one wave with 2..32 elements per
-# lane, workgroups of 4 / 16 waves with 16..64 elements per lane, and the
-# two-pass stream, at the edges of each
+# lane, workgroups of 4 / 16 waves with 16..64 elements per lane, rows split
+# over workgroups (aligned lengths from 8196 on: 16384, 32768, 65536, 200000)
+# and the two-pass stream, at the edges of each
 COLS = [1, 2, 3, 5, 8, 10, 16, 17, 31, 32, 33, 63, 64, 65, 100, 128, 129, 255, 256, 257, 500, 512, 513, 1000,
         1024, 1025, 2047, 2048, 2049, 4095, 4096, 4097, 8192, 8193, 10000, 16384, 16385, 32768, 32769, 65535,
         65536, 65537, 200000]
@@ -100,6 +101,54 @@ def test_large_magnitudes_and_infinities(capi, cols):
     err = orc.max_rel_err(y[keep], ref[keep])
     _say(f"  finite rows: max-rel-err {err:.3e}")
     assert err <= TOL
+
+
+# Rows split over workgroups that exchange (max, sum) partials through device
+# memory (16-byte aligned rows of 8193 .. 2 Mi columns): 3, 16, 32 and 64
+# chunks, a ragged last chunk, and the first length past the split range
+# (the two-pass stream kernel).
+@pytest.mark.parametrize("rows,cols", [(40, 12288), (6, 262144), (3, 1048576), (2, 2097152), (2, 2097156),
+                                       (7, 1000004)])
+def test_split_rows(capi, rows, cols):
+    _say(f"softmax split rows={rows} cols={cols}")
+    x = (np.random.default_rng(cols + rows).standard_normal((rows, cols)) * 3).astype(np.float32)
+    _check(f"[{rows}, {cols}]", _softmax_gpu(capi, x), x)
+
+
+def test_split_grid_far_beyond_the_resident_workgroups(capi):
+    # 4000 rows x 3 chunks = 12000 workgroups: rows wait for chunks that are
+    # dispatched only after earlier rows have finished
+    rows, cols = 4000, 12288
+    _say(f"softmax split rows={rows} cols={cols} (grid beyond the resident workgroups)")
+    x = np.random.default_rng(99).standard_normal((rows, cols)).astype(np.float32)
+    _check(f"[{rows}, {cols}]", _softmax_gpu(capi, x), x)
+
+
+def test_split_chunks_without_a_finite_value_and_nan(capi):
+    cols = 65536  # 8 chunks of 8192 columns
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal((5, cols)) * 4).astype(np.float32)
+    x[0, 8192:3 * 8192] = -np.inf     # two whole chunks masked: exact zeros there, the rest as usual
+    x[1, :cols - 8192] = -np.inf      # only the last chunk finite
+    x[2, 20000] = np.nan              # NaN in one chunk -> the whole row NaN
+    x[3, :] = -np.inf                 # every chunk masked -> NaN row
+    y = _softmax_gpu(capi, x)
+    ref = orc.softmax_rows_f64(x)
+    assert (y[0, 8192:3 * 8192] == 0).all() and (y[1, :cols - 8192] == 0).all()
+    assert np.isnan(y[2]).all() and np.isnan(y[3]).all()
+    err = orc.max_rel_err(y[[0, 1, 4]], ref[[0, 1, 4]])
+    _say(f"  finite rows: max-rel-err {err:.3e}")
+    assert err <= TOL
+
+
+def test_split_repeated_calls_reuse_the_partials_buffer(capi):
+    """Consecutive calls on one stream reuse the slot buffer with a new
+    generation each: stale partials of an earlier call (other values, another
+    chunk layout) must never be taken for the current ones."""
+    rng = np.random.default_rng(12)
+    for rows, cols in [(64, 65536), (64, 65536), (32, 131072), (200, 16384), (64, 65536)]:
+        x = (rng.standard_normal((rows, cols)) * 2 + rng.standard_normal()).astype(np.float32)
+        _check(f"repeat [{rows}, {cols}]", _softmax_gpu(capi, x), x)
 
 
 def test_layer_softmax_forward_matches_oracle():
