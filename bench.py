@@ -215,6 +215,12 @@ GPU_CONFIGS = {
     3: GpuConfig(3, 16, 16, 1024, 1024, 64, "bf16", True, True, 0.5),
     5: GpuConfig(5, C5["B"], C5["H"], C5["L"], C5["L"], C5["d"], "bf16", True, True),
 }
+# Supported shapes outside BASELINE.json's configurations, timed beside them
+# (not graded): fp32 at the largest head dim, causal and not.
+EXTRA_CONFIGS = {
+    "f32_d128_causal": GpuConfig(0, 2, 16, 2048, 2048, 128, "f32", True, True),
+    "f32_d128": GpuConfig(0, 2, 16, 2048, 2048, 128, "f32", False, True),
+}
 
 
 def config_flops(cfg):
@@ -755,6 +761,15 @@ def main(argv=None):
                 line["cpu_baseline"] = config_cpu_baseline(cfg, max_heads={1: 1, 2: 64, 3: 32}[cid])
             lines.append(line)
         out["configs"] = lines
+        extra = []
+        for name, cfg in EXTRA_CONFIGS.items():
+            ms = run_config(T, cfg, max(args.steps, 20), args.warmup)
+            tf = config_flops(cfg) / (ms * 1e-3) / 1e12
+            extra.append({"config": name, "workload": f"{'causal ' if cfg.causal else ''}attention fwd+bwd f32, "
+                                                      f"B={cfg.B} H={cfg.H} L={cfg.Lq} d={cfg.d} (not a BASELINE config)",
+                          "dtype": "f32", "flop_per_step": config_flops(cfg), "ms_per_step": ms, "value": tf,
+                          "unit": "TFLOP/s", "peak": PEAK_FP32_MFMA_TFLOPS, "frac_of_peak": tf / PEAK_FP32_MFMA_TFLOPS})
+        out["extra_configs"] = extra
 
     if args.only in ("all", "softmax"):
         cases = []

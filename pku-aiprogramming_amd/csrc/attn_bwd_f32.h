@@ -13,13 +13,18 @@
 namespace tt {
 
 constexpr int BWD_F32_BN = 128;  // keys per dK/dV workgroup
-constexpr int BWD_F32_BQ = 64;   // queries per LDS step of the dK/dV kernel
 constexpr int BWD_F32_BM = 128;  // queries per dQ workgroup
 constexpr int BWD_F32_KN = 64;   // keys per LDS step of the dQ kernel
+// Queries per LDS step of the dK/dV role: 64, or 32 at d = 128, where a lane
+// already holds 64 floats of its key's K row, 64 of its V row and 128
+// accumulators, and the register-staged prefetch of two 64-query tiles (64
+// more) made the causal kernel spill 61 VGPRs.
+template <int D>
+constexpr int bwd_f32_bq() { return D >= 128 ? 32 : 64; }
 
 // LDS floats of each role: Q and dO tiles plus their LSE / -D rows; K and V tiles.
 template <int D>
-constexpr int bwd_f32_dkdv_lds() { return 2 * BWD_F32_BQ * (D + 1) + 2 * BWD_F32_BQ; }
+constexpr int bwd_f32_dkdv_lds() { return 2 * bwd_f32_bq<D>() * (D + 1) + 2 * bwd_f32_bq<D>(); }
 template <int D>
 constexpr int bwd_f32_dq_lds() { return 2 * BWD_F32_KN * (D + 1); }
 
@@ -32,10 +37,11 @@ __device__ __forceinline__ void bwd_f32_dkdv(int id, float* smem, const float* _
                                              const float* __restrict__ NDelta, float* __restrict__ dK,
                                              float* __restrict__ dV, int Lq, int Lk, int BH, int nkt, int group,
                                              float sl2, float scale) {
-  constexpr int BN = BWD_F32_BN, BQ = BWD_F32_BQ;
+  constexpr int BN = BWD_F32_BN, BQ = bwd_f32_bq<D>(), MT = BQ / 32;
   constexpr int P = D + 1;
   constexpr int NC = D / 2, ND = D / 32, CPR = D / 4;
   constexpr int LPT = BQ * CPR / 256;
+  static_assert(BQ * CPR % 256 == 0 && BQ <= 256, "a query tile splits evenly over the 256 threads");
   float* sQ = smem;
   float* sdO = sQ + BQ * P;
   float* sL = sdO + BQ * P;
@@ -108,7 +114,7 @@ __device__ __forceinline__ void bwd_f32_dkdv(int id, float* smem, const float* _
     if (qb + BQ < Lq) gload(qb + BQ);
     if (CAUSAL && qb + BQ - 1 < wk_lo) continue;
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
+    for (int mt = 0; mt < MT; ++mt) {
       f32x16 s = f32x16{}, dp = f32x16{};
 #pragma unroll
       for (int c = 0; c < NC; ++c) {

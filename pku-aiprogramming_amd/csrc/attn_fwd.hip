@@ -586,14 +586,17 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void attn_fwd_f32_kernel(
   const int kb_lo = min(kend, split * per), kb_hi = min(kend, kb_lo + per);
   const int wq_lo = q0 + 32 * w, wq_hi = wq_lo + 31;
 
-  float4 kreg[LPT], vreg[LPT];
+  // The staged tile rows are native 4-float vectors: copies of the float4
+  // struct kept this array in scratch memory (a private-memory round trip per
+  // tile) instead of registers.
+  f32x4 kreg[LPT], vreg[LPT];
   auto gload = [&](int kb) {
 #pragma unroll
     for (int i = 0; i < LPT; ++i) {
       const int c = tid + 256 * i;
       const int row = min(kb + c / CPR, Lk - 1), ch = c % CPR;  // rows past Lk are masked
-      kreg[i] = *reinterpret_cast<const float4*>(K + kbase + (int64_t)row * D + 4 * ch);
-      vreg[i] = *reinterpret_cast<const float4*>(V + kbase + (int64_t)row * D + 4 * ch);
+      kreg[i] = *reinterpret_cast<const f32x4*>(K + kbase + (int64_t)row * D + 4 * ch);
+      vreg[i] = *reinterpret_cast<const f32x4*>(V + kbase + (int64_t)row * D + 4 * ch);
     }
   };
   auto sstore = [&]() {
@@ -601,7 +604,7 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void attn_fwd_f32_kernel(
     for (int i = 0; i < LPT; ++i) {
       const int c = tid + 256 * i;
       const int key = c / CPR, ch = c % CPR;  // d-indices 4ch .. 4ch + 3
-      *reinterpret_cast<float4*>(&sK[key * PK + 4 * ch]) = kreg[i];
+      *reinterpret_cast<f32x4*>(&sK[key * PK + 4 * ch]) = kreg[i];
       float* pv = &sV[4 * ch * PV + key];
       pv[0] = vreg[i].x;
       pv[PV] = vreg[i].y;
