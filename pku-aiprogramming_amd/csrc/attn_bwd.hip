@@ -336,23 +336,15 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_b
   run(max(qdiag, qfull), Lq, std::true_type{});
   wait_vmem_le<0>();  // nothing may be in flight into LDS when the workgroup exits
 
-  if (key < Lk) {
-    u16* dkrow = dK + kbase + (int64_t)key * D;
-    u16* dvrow = dV + kbase + (int64_t)key * D;
-#pragma unroll
-    for (int dt = 0; dt < ND; ++dt)
-#pragma unroll
-      for (int r = 0; r < 16; r += 4) {
-        const int d0 = 32 * dt + acc_row(r, g);
-        uint2 a, b;
-        a.x = pack_bf16x2(adk[dt][r] * scale, adk[dt][r + 1] * scale);
-        a.y = pack_bf16x2(adk[dt][r + 2] * scale, adk[dt][r + 3] * scale);
-        b.x = pack_bf16x2(adv[dt][r], adv[dt][r + 1]);
-        b.y = pack_bf16x2(adv[dt][r + 2], adv[dt][r + 3]);
-        *reinterpret_cast<uint2*>(dkrow + d0) = a;
-        *reinterpret_cast<uint2*>(dvrow + d0) = b;
-      }
-  }
+  // dK (scaled), then dV, through LDS: rows 0 .. BN - 1 and BN .. 2 BN - 1
+  static_assert(2 * BN * D * 2 <= kLds, "the LDS block holds the workgroup's dK and dV rows");
+  u16* const stage = reinterpret_cast<u16*>(smem);
+  __syncthreads();
+  stage_rows_bf16<D, ND>(stage, 32 * w + r32, g, adk, scale);
+  stage_rows_bf16<D, ND>(stage + BN * D, 32 * w + r32, g, adv, 1.f);
+  __syncthreads();
+  store_staged_rows<D>(stage, BN, dK + kbase, k0, Lk, 64 * NW);
+  store_staged_rows<D>(stage + BN * D, BN, dV + kbase, k0, Lk, 64 * NW);
 }
 
 // ------------------------------------------------------------------ bf16 dQ
@@ -694,18 +686,12 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_pipe_kernel(
   }
   wait_vmem_le<0>();  // nothing may be in flight into LDS when the workgroup exits
 
-  if (qrow < Lq) {
-    u16* row = dQ + qbase + (int64_t)qrow * D;
-#pragma unroll
-    for (int dt = 0; dt < ND; ++dt)
-#pragma unroll
-      for (int r = 0; r < 16; r += 4) {
-        uint2 v;
-        v.x = pack_bf16x2(adq[dt][r] * scale, adq[dt][r + 1] * scale);
-        v.y = pack_bf16x2(adq[dt][r + 2] * scale, adq[dt][r + 3] * scale);
-        *reinterpret_cast<uint2*>(row + 32 * dt + acc_row(r, g)) = v;
-      }
-  }
+  // dQ through LDS: the ring is free once every wave has passed its wait
+  static_assert(2 * S * TE >= BM * D, "the tile ring holds the workgroup's dQ rows");
+  __syncthreads();
+  stage_rows_bf16<D, ND>(smem, 32 * w + r32, g, adq, scale);
+  __syncthreads();
+  store_staged_rows<D>(smem, BM, dQ + qbase, q0, Lq, 64 * NW);
 }
 
 // ------------------------------------------------------------------ launchers

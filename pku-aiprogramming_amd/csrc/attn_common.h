@@ -171,6 +171,43 @@ struct SwzTile {
   __device__ static __forceinline__ int at4(int row, int col) { return chunk(row, col >> 3) + (col & 4); }
 };
 
+// Output epilogue through LDS.  An MFMA kernel whose lane (r32, g) holds, in
+// accumulator tile dt, columns 32 dt + acc_row(r, g) (r = 0..15) of output
+// row `row` writes those values to LDS as bf16 (scaled by `mul`), four
+// columns per 8-byte write, in the SwzTile layout; after a barrier every
+// thread copies whole 16-byte chunks to global memory, so one store
+// instruction writes 1 KB of contiguous rows.  Written straight from the
+// accumulators, each 8-byte store instruction touches 32 rows, and the
+// epilogue of a workgroup took 1-2.5 us on the MI355X.
+template <int D, int ND>
+__device__ __forceinline__ void stage_rows_bf16(u16* stage, int row, int g, const f32x16 (&acc)[ND], float mul) {
+  using Tile = SwzTile<D>;
+#pragma unroll
+  for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+    for (int r = 0; r < 16; r += 4) {
+      uint2 v;
+      v.x = pack_bf16x2(acc[dt][r] * mul, acc[dt][r + 1] * mul);
+      v.y = pack_bf16x2(acc[dt][r + 2] * mul, acc[dt][r + 3] * mul);
+      *reinterpret_cast<uint2*>(&stage[Tile::at4(row, 32 * dt + acc_row(r, g))]) = v;
+    }
+}
+// Rows [0, nrows) of `stage` to rows row0 + i of the row-major [., D] matrix
+// at `dst`, skipping rows >= rmax; `nthreads` threads of the workgroup.
+template <int D>
+__device__ __forceinline__ void store_staged_rows(const u16* stage, int nrows, u16* dst, int row0, int rmax,
+                                                  int nthreads) {
+  using Tile = SwzTile<D>;
+  constexpr int CPR = D / 8;
+#pragma unroll 4
+  for (int c = threadIdx.x; c < nrows * CPR; c += nthreads) {
+    const int row = c / CPR, ch = c - row * CPR;
+    if (row0 + row < rmax)
+      *reinterpret_cast<uint4*>(dst + (int64_t)(row0 + row) * D + 8 * ch) =
+          *reinterpret_cast<const uint4*>(&stage[Tile::chunk(row, ch)]);
+  }
+}
+
 typedef __attribute__((address_space(3))) void lds_void;
 
 // LDS byte address of a pointer into a __shared__ array.

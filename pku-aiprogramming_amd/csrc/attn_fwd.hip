@@ -509,20 +509,28 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fwd_bf16_pipe_kernel(
   wait_vmem_le<0>();  // nothing may be in flight into LDS when the workgroup exits
 
   const float ls = sum_xor32(lsum);
-  if (qrow < Lq) {
-    const float inv = ls > 0.f ? 1.f / ls : 0.f;
+  const float inv = ls > 0.f ? 1.f / ls : 0.f;
+  if (qrow < Lq && g == 0 && LSE) LSE[(int64_t)bh * Lq + qrow] = (m + __log2f(ls)) * kLn2;
+  if constexpr (D >= 128) {
+    // O through LDS (the K ring is free once every wave has passed its last
+    // wait; 128 rows of D bf16 fit the two K buffers): c5 -0.5 %; at d = 64
+    // the two extra barriers cost more than the 8-byte stores (+1.7 % at c3)
+    static_assert(2 * TE >= BM * D, "the K ring holds the workgroup's O rows");
+    __syncthreads();
+    stage_rows_bf16<D, ND>(sK, 32 * w + r32, g, o, inv);
+    __syncthreads();
+    store_staged_rows<D>(sK, BM, O + qbase, q0, Lq, 64 * NW);
+  } else if (qrow < Lq) {
     u16* orow = O + qbase + (int64_t)qrow * D;
 #pragma unroll
     for (int dt = 0; dt < ND; ++dt)
 #pragma unroll
       for (int r = 0; r < 16; r += 4) {
-        const int d0 = 32 * dt + acc_row(r, g);
         uint2 v;
         v.x = pack_bf16x2(o[dt][r] * inv, o[dt][r + 1] * inv);
         v.y = pack_bf16x2(o[dt][r + 2] * inv, o[dt][r + 3] * inv);
-        *reinterpret_cast<uint2*>(orow + d0) = v;
+        *reinterpret_cast<uint2*>(orow + 32 * dt + acc_row(r, g)) = v;
       }
-    if (g == 0 && LSE) LSE[(int64_t)bh * Lq + qrow] = (m + __log2f(ls)) * kLn2;
   }
 }
 
