@@ -49,9 +49,9 @@ C4 = dict(B=64, H=32, Lkv=8192, d=128)
 # write x1.000); the commands and raw counters are in
 # profiles/hbm_traffic_c5_c4.md.  Re-measured whenever a kernel changes.
 MEASURED_TRAFFIC_MIB = {
-    "attn_fwd": 539.1,
-    "attn_bwd_dq": 881.2,      # also the row pre-pass: reads O, writes -D and LSE log2(e)
-    "attn_bwd_dkdv": 966.1,    # the persistent 256-key kernel at d = 128
+    "attn_fwd": 555.8,
+    "attn_bwd_dq": 883.8,      # also the row pre-pass: reads O, writes -D and LSE log2(e)
+    "attn_bwd_dkdv": 1020.1,   # the persistent 256-key kernel at d = 128
     "attn_decode_split": 8193.2,
     "softmax_reg": 2048.1,      # k_softmax_reg<16>, 262144 x 1024 fp32 (profiles/softmax_rows_kernel_stats.md)
     "gemm_bf16_nn": 2527.8 + 149.6,  # k_gemm_dma 8192^3 NN (profiles/gemm_kernel_stats.md)
