@@ -569,6 +569,16 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_pipe_kernel(
   f32x16 adq[ND];
 #pragma unroll
   for (int dt = 0; dt < ND; ++dt) adq[dt] = f32x16{};
+  // At d <= 64 the dP^T accumulator starts at -D of the lane's query (16
+  // registers holding ndl), so the MFMAs yield dP - D and forming dS takes
+  // one VALU operation less per score; at d = 128 the kernel has no 16
+  // registers to spare and adds -D itself.
+  constexpr bool kDpInit = D <= 64;
+  f32x16 dinit = f32x16{};
+  if constexpr (kDpInit) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dinit[r] = ndl;
+  }
 
   // Last block this wave computes: its diagonal block (causal) or the last
   // one.  Every earlier block lies inside Lk and before every query of the
@@ -601,7 +611,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_pipe_kernel(
       const bf16x8 ka = *reinterpret_cast<const bf16x8*>(&tK[kidx[c]]);
       const bf16x8 va = *reinterpret_cast<const bf16x8*>(&tK[TE + kidx[c]]);
       s = mfma_bf16_32x32x16(ka, qf[c], c == 0 ? f32x16{} : s);
-      dp = mfma_bf16_32x32x16(va, dof[c], c == 0 ? f32x16{} : dp);
+      dp = mfma_bf16_32x32x16(va, dof[c], c == 0 ? dinit : dp);
     }
   };
   // dS^T of the block at keys kb in ring buffer B, then dQ^T += K^T dS^T
@@ -617,7 +627,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_pipe_kernel(
         const int key = kb + acc_row(r, g);
         if (key >= Lk || (CAUSAL && key > qrow)) p = 0.f;
       }
-      db[r >> 3][r & 7] = (__bf16)(p * (dp[r] + ndl));
+      db[r >> 3][r & 7] = (__bf16)(p * (kDpInit ? dp[r] : dp[r] + ndl));
     }
     const u16* tK = smem + 2 * B * TE;
 #pragma unroll
