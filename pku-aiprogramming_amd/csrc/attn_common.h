@@ -67,16 +67,24 @@ __device__ __forceinline__ float wave_xor32(float x) { return __shfl_xor(x, 32, 
 // 0..31 of x in both halves and r[1] = lanes 32..63 in both halves (checked
 // on the MI355X).  Both halves compute the same expression, so they agree
 // bit for bit.
+// Maximum of two floats that propagates NaN (IEEE 754-2019 maximum): on gfx950
+// v_maximum_f32 / v_maximum3_f32.  fmaxf (maxNum) in the kernels' IEEE mode
+// quiets each operand the compiler cannot prove canonical first, one
+// v_max_f32 x, x, x per MFMA result or cross-lane value it reads (11 extra VALU
+// operations per tile in the forward's row max); a NaN score gives a NaN row
+// either way.
+__device__ __forceinline__ float vmax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+__device__ __forceinline__ float vmax3(float a, float b, float c) { return vmax(vmax(a, b), c); }
+
 __device__ __forceinline__ float max_xor32(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  return vmax(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 __device__ __forceinline__ float sum_xor32(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-__device__ __forceinline__ float fmax3(float a, float b, float c) { return fmaxf(fmaxf(a, b), c); }
 
 // acc + the two bf16 halves of element e (a bf16 pair) of v, by one
 // v_dot2_f32_bf16 against (1, 1).

@@ -135,14 +135,14 @@ __global__ __launch_bounds__(64 * fwd_nw(D), 8 / fwd_nw(D)) void attn_fwd_bf16_k
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[t][r]);
-    mx = fmaxf(mx, wave_xor32(mx)) * sl2;
+      for (int r = 0; r < 16; ++r) mx = vmax(mx, s[t][r]);
+    mx = vmax(mx, wave_xor32(mx)) * sl2;
     // Lazy rescale: the running max only moves when some lane's tile max
     // exceeds it by more than 8 (log2 units), so p = 2^(x - m) <= 256 and the
     // O / sum rescale is skipped on most tiles.  The result is exact either
     // way: numerator and denominator share the same m.
     if (wave_any(mx > m + 8.f)) {
-      const float mnew = fmaxf(m, mx);
+      const float mnew = vmax(m, mx);
       const float alpha = fast_exp2(m - mnew);  // 0 when m = -inf
       lsum *= alpha;
 #pragma unroll
@@ -342,17 +342,17 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fwd_bf16_pipe_kernel(
     float x[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      x[c] = fmaxf(s[c >> 1][8 * (c & 1)], s[c >> 1][8 * (c & 1) + 1]);
+      x[c] = vmax(s[c >> 1][8 * (c & 1)], s[c >> 1][8 * (c & 1) + 1]);
 #pragma unroll
-      for (int r = 2; r < 8; r += 2) x[c] = fmax3(x[c], s[c >> 1][8 * (c & 1) + r], s[c >> 1][8 * (c & 1) + r + 1]);
+      for (int r = 2; r < 8; r += 2) x[c] = vmax3(x[c], s[c >> 1][8 * (c & 1) + r], s[c >> 1][8 * (c & 1) + r + 1]);
     }
-    const float mx = max_xor32(fmaxf(fmax3(x[0], x[1], x[2]), x[3])) * sl2;
+    const float mx = max_xor32(vmax(vmax3(x[0], x[1], x[2]), x[3])) * sl2;
     if (first) {
       m = mx;
       return false;
     }
     const bool need = wave_any(mx > m + 8.f);
-    const float mn = need ? fmaxf(m, mx) : m;
+    const float mn = need ? vmax(m, mx) : m;
     alpha = fast_exp2(m - mn);  // exactly 1 when m is unchanged; 0 when m was -inf
     m = mn;
     lsum *= alpha;
@@ -655,10 +655,10 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void attn_fwd_f32_kernel(
           if (key >= Lk || (CAUSAL && key > qrow)) x = -INFINITY;
         }
         s[t][r] = x;
-        mx = fmaxf(mx, x);
+        mx = vmax(mx, x);
       }
-    mx = fmaxf(mx, wave_xor32(mx));
-    const float mnew = fmaxf(m, mx);
+    mx = vmax(mx, wave_xor32(mx));
+    const float mnew = vmax(m, mx);
     const float mb = (mnew == -INFINITY) ? 0.f : mnew;
     const float alpha = fast_exp2(m - mb);
     m = mnew;
