@@ -252,10 +252,15 @@ int tt_attn_decode_f32(const float* q, const float* k, const float* v, float* o,
  *   y[r][c] = exp(x[r][c] - m_r) / sum_c' exp(x[r][c'] - m_r),  m_r = max_c x[r][c].
  * Replaces SoftmaxForward (src/Layers.cu:324-349: cudaChannelMax, Sub, Exp,
  * Sum, Div of src/Layers_kernels.cu:189-257, the max and the sum each a host
- * loop of thrust calls per row) with one kernel: rows up to 2048 columns are
- * read once into registers, longer rows are read twice.  y may alias x.
- * A row of -inf (or holding +inf or NaN) gives NaN, as the reference's
- * x - max does. */
+ * loop of thrust calls per row) with one kernel that reads each element once
+ * into registers and writes it once: a wave per row up to 2048 columns, a
+ * workgroup per row up to 8192 (65536 for rows that are not 16-byte
+ * aligned), and for aligned rows of 8196 .. 2 Mi columns 2-64 workgroups per
+ * row that merge their (max, sum) partials through a per-stream library
+ * workspace of rows x chunks x 16 bytes (allocated on first use,
+ * TT_ERR_NOMEM if that fails; calls on one stream share it in order).
+ * Longer rows are read twice.  y may alias x.  A row of -inf (or holding
+ * +inf or NaN) gives NaN, as the reference's x - max does. */
 int tt_softmax_rows_f32(const float* x, float* y, int64_t rows, int64_t cols, void* stream);
 
 /* ---------------------------------------------------------------- GEMM */

@@ -725,7 +725,8 @@ static int launch_bwd(const T* q, const T* k, const T* v, const T* o, const floa
     constexpr int NW = bwd_nw(D);
     const int64_t nkt = (Lk + 32 * NW - 1) / (32 * NW);
     const int64_t nqp = (Lq + 127) / 128;
-    if (nkt * BH > 0x7fffffff || nqp * BH > 0x7fffffff) return fail(TT_ERR_ARG, "attention backward: grid too large");
+    if (!grid_fits(nkt * BH, 64 * NW) || !grid_fits(nqp * BH, 256))
+      return fail(TT_ERR_ARG, "attention backward: grid too large");
     const int gp = pick_group(BH, nqp, 32 * 2), gk = pick_group(BH, nkt, 32 * 8 / NW);
     hipLaunchKernelGGL((attn_bwd_dq_pipe_kernel<D, CAUSAL>), dim3((unsigned)(nqp * BH)), dim3(256), 0, st, q, k, v, o,
                        dout, lse, l2, delta, dq, (int)Lq, (int)Lk, (int)BH, (int)nqp, gp, sl2, scale);
@@ -740,7 +741,7 @@ static int launch_bwd(const T* q, const T* k, const T* v, const T* o, const floa
   } else {
     constexpr int TPR = D / (16 / (int)sizeof(T));
     const int64_t dblk = (rows + (256 / TPR) - 1) / (256 / TPR);
-    if (dblk > 0x7fffffff) return fail(TT_ERR_ARG, "attention backward: grid too large");
+    if (!grid_fits(dblk, 256)) return fail(TT_ERR_ARG, "attention backward: grid too large");
     hipLaunchKernelGGL((attn_bwd_delta_kernel<T, D>), dim3((unsigned)dblk), dim3(256), 0, st, o, dout, lse, delta,
                        l2, rows);
     TT_LAUNCHED("attention backward delta launch", st);
@@ -749,7 +750,8 @@ static int launch_bwd(const T* q, const T* k, const T* v, const T* o, const floa
       constexpr int NW = bwd_nw(D);
       const int64_t nkt = (Lk + 32 * NW - 1) / (32 * NW);
       const int64_t nqt = (Lq + 32 * NW - 1) / (32 * NW);
-      if (nkt * BH > 0x7fffffff || nqt * BH > 0x7fffffff) return fail(TT_ERR_ARG, "attention backward: grid too large");
+      if (!grid_fits(nkt * BH, 64 * NW) || !grid_fits(nqt * BH, 64 * NW))
+        return fail(TT_ERR_ARG, "attention backward: grid too large");
       // heads in flight per XCD: tiles for the resident workgroups of its 32 CUs
       const int gk = pick_group(BH, nkt, 32 * 8 / NW), gq = pick_group(BH, nqt, 32 * 8 / NW);
       hipLaunchKernelGGL((attn_bwd_dkdv_bf16_kernel<D, CAUSAL>), dim3((unsigned)(nkt * BH)), dim3(64 * NW), 0, st, q,
@@ -761,7 +763,7 @@ static int launch_bwd(const T* q, const T* k, const T* v, const T* o, const floa
     } else {
       const int64_t nkt = (Lk + BWD_F32_BN - 1) / BWD_F32_BN;
       const int64_t nqt = (Lq + BWD_F32_BM - 1) / BWD_F32_BM;
-      if ((nkt + nqt) * BH > 0x7fffffff) return fail(TT_ERR_ARG, "attention backward: grid too large");
+      if (!grid_fits((nkt + nqt) * BH, 256)) return fail(TT_ERR_ARG, "attention backward: grid too large");
       const int gk = pick_group(BH, nkt, 32), gq = pick_group(BH, nqt, 32);
       hipLaunchKernelGGL((attn_bwd_f32_kernel<D, CAUSAL>), dim3((unsigned)((nkt + nqt) * BH)), dim3(256), 0, st,
                          q, k, v, dout, lse, delta, dq, dk, dv, (int)Lq, (int)Lk, (int)BH, (int)nkt, (int)nqt,

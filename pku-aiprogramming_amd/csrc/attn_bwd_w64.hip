@@ -564,7 +564,7 @@ int launch_dkdv_w64(const u16* q, const u16* k, const u16* v, const u16* dout, c
                     u16* dk, u16* dv, int64_t BH, int64_t Lq, int64_t Lk, float sl2, float scale, bool causal,
                     hipStream_t st) {
   const int64_t nkt = (Lk + DKW_BN - 1) / DKW_BN;
-  if (nkt * BH > 0x7fffffff) return fail(TT_ERR_ARG, "attention backward: grid too large");
+  if (!grid_fits(nkt * BH, 256)) return fail(TT_ERR_ARG, "attention backward: grid too large");
   // one workgroup per CU (the LDS block allows no second), each through its share of the items
   const int64_t cus = device_cu_count(), items = nkt * BH;
   const int G = (int)(items < cus ? items : cus);

@@ -218,7 +218,7 @@ static int launch_decode(const T* q, const T* k, const T* v, T* o, float* lse, i
     }
   if (Lkv < chunk) chunk = (int)((Lkv + 63) / 64 * 64);
   const int64_t nsplit = (Lkv + chunk - 1) / chunk;
-  if (BH * nsplit > 0x7fffffff) return fail(TT_ERR_ARG, "attention decode: grid too large");
+  if (!grid_fits(BH * nsplit, DEC_THREADS)) return fail(TT_ERR_ARG, "attention decode: grid too large");
   const float sl2 = scale * kLog2e;
   const dim3 grid((unsigned)(nsplit * BH)), block(DEC_THREADS);
   if (nsplit == 1) {  // one split per head: no partials, no combine

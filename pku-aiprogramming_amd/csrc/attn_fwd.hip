@@ -753,7 +753,7 @@ static int launch_fwd(KernelPtr kern, int bm, int threads, int wg_per_cu, const 
                       T* o, float* lse, int64_t BH, int64_t Lq, int64_t Lk, float scale, hipStream_t s) {
   const int64_t nqt = (Lq + bm - 1) / bm;
   const int64_t nblk = nqt * BH;
-  if (nblk > 0x7fffffff) return fail(TT_ERR_ARG, "attention forward: grid too large");
+  if (!grid_fits(nblk, threads)) return fail(TT_ERR_ARG, "attention forward: grid too large");
   // heads in flight per XCD: enough tiles for the resident workgroups of its
   // 32 CUs
   const int group = pick_group(BH, nqt, 32 * wg_per_cu);
@@ -791,7 +791,7 @@ static int fwd_f32(const float* q, const float* k, const float* v, float* o, flo
   if (nsplit > 4) nsplit = 4;
   if (nsplit > ktiles) nsplit = ktiles;
   if (nsplit < 1) nsplit = 1;
-  if (ntq * nsplit > 0x7fffffff) return fail(TT_ERR_ARG, "attention forward: grid too large");
+  if (!grid_fits(ntq * nsplit, 256)) return fail(TT_ERR_ARG, "attention forward: grid too large");
   const int group = pick_group(BH, nqt, 32 * wg_per_cu);
   const float sl2 = scale * kLog2e;
   if (nsplit == 1) {

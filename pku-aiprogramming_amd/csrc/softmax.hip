@@ -359,7 +359,7 @@ extern "C" int tt_softmax_rows_f32(const float* x, float* y, int64_t rows, int64
   if (aligned && cols > 8192 && cols <= int64_t(kSplitMaxChunks) * 32768) {
     const int ne4 = cols <= 16384 ? 4 : cols <= 65536 ? 8 : cols <= 262144 ? 16 : 32;
     const int64_t cw = 1024 * ne4, nchunk = (cols + cw - 1) / cw;
-    if (rows * nchunk <= 0x7fffffff) {
+    if (grid_fits(rows * nchunk, kBlock)) {  // else the grid-stride kernels below
       unsigned long long* slots = nullptr;
       uint64_t uses = 0;
       const size_t bytes = (size_t)(rows * nchunk) * 2 * sizeof(unsigned long long);

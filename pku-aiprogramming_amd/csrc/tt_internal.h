@@ -68,6 +68,14 @@ class WorkspaceLease {
     if (e_ != hipSuccess) return tt::hip_fail(e_, what);       \
   } while (0)
 
+namespace tt {
+// A one-dimensional launch holds at most 2^32 - 1 work-items (the dispatch
+// packet counts the grid in work-items, not workgroups).
+inline bool grid_fits(int64_t workgroups, int64_t threads) {
+  return workgroups >= 0 && workgroups <= int64_t(0xffffffffu) / threads;
+}
+}  // namespace tt
+
 // Launch-error check plus the instrumentation hook, for kernels on stream s.
 #define TT_LAUNCHED(what, s)    \
   do {                          \

@@ -462,7 +462,7 @@ int tt_read_probe(const void* buf, int64_t bytes, float* out, void* stream) {
   if (rc) return rc;
   const int64_t n16 = bytes / 16, chunk16 = (int64_t(256) << 10) / 16;
   const int64_t nb = (n16 + chunk16 - 1) / chunk16;
-  if (nb > 0x7fffffff) return fail(TT_ERR_ARG, "tt_read_probe: too large");
+  if (!grid_fits(nb, 256)) return fail(TT_ERR_ARG, "tt_read_probe: too large");
   hipStream_t s = stream_or_default(stream);
   hipLaunchKernelGGL(k_read_probe, dim3((unsigned)nb), dim3(256), 0, s, (const probe_u32x4*)buf, n16, chunk16, out);
   TT_LAUNCHED("read probe launch", s);

@@ -151,6 +151,20 @@ def test_split_repeated_calls_reuse_the_partials_buffer(capi):
         _check(f"repeat [{rows}, {cols}]", _softmax_gpu(capi, x), x)
 
 
+def test_split_random_shapes(capi):
+    """Seeded random aligned lengths, log-uniform over the whole split range
+    (4 Ki .. 32 Ki column chunks, ragged last chunks of any multiple of 4
+    columns), random row counts, scales and offsets."""
+    rng = np.random.default_rng(2024)
+    for i in range(12):
+        cols = 4 * int(np.exp(rng.uniform(np.log(8196 // 4), np.log(2 * 1024 * 1024 // 4))))
+        rows = int(rng.integers(1, max(2, 6_000_000 // cols) + 1))
+        scale, shift = float(rng.uniform(0.5, 8)), float(rng.uniform(-50, 50))
+        _say(f"softmax split random #{i}: rows={rows} cols={cols} scale={scale:.2f} shift={shift:.1f}")
+        x = (rng.standard_normal((rows, cols)) * scale + shift).astype(np.float32)
+        _check(f"random [{rows}, {cols}]", _softmax_gpu(capi, x), x)
+
+
 def test_layer_softmax_forward_matches_oracle():
     """myLayer.SoftmaxForward(input, output) as the reference's cross-entropy
     caller uses it (optimizer/operators.py:642-647): [batch, 10] on "gpu";
