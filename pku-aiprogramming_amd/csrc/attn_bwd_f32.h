@@ -18,7 +18,9 @@ constexpr int BWD_F32_KN = 64;   // keys per LDS step of the dQ kernel
 // Queries per LDS step of the dK/dV role: 64, or 32 at d = 128, where a lane
 // already holds 64 floats of its key's K row, 64 of its V row and 128
 // accumulators, and the register-staged prefetch of two 64-query tiles (64
-// more) made the causal kernel spill 61 VGPRs.
+// more) made the causal kernel spill 61 VGPRs to scratch memory (232 bytes
+// per lane); with 32-query tiles no scratch is used (36 VGPRs are parked in
+// unused AGPRs instead).
 template <int D>
 constexpr int bwd_f32_bq() { return D >= 128 ? 32 : 64; }
 
