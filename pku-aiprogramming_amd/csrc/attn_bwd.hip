@@ -95,7 +95,7 @@ template <int D, bool CAUSAL>
 __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_bf16_kernel(
     const u16* __restrict__ Q, const u16* __restrict__ K, const u16* __restrict__ V,
     const u16* __restrict__ dO, const float* __restrict__ L2, const float* __restrict__ NDelta,
-    u16* __restrict__ dK, u16* __restrict__ dV, int Lq, int Lk, int BH, int nkt, int group, float sl2,
+    u16* __restrict__ dK, u16* __restrict__ dV, int Lq, int Lk, int BH, int nkt, int order, float sl2,
     float scale) {
   using Tile = SwzTile<D>;
   constexpr int NW = bwd_nw(D), BN = 32 * NW, BQ = kDkdvBQ, MT = BQ / 32, S = kBwdStages;
@@ -123,7 +123,7 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_b
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63, g = l >> 5, r32 = l & 31;
   const int wu = __builtin_amdgcn_readfirstlane(w);  // w, known wave-uniform (scalar branches)
   int kt, bh;
-  map_tile(blockIdx.x, nkt, BH, group, kt, bh, false);  // causal: key tile 0 sees every query
+  map_tile(blockIdx.x, nkt, BH, order, kt, bh, false);  // causal: key tile 0 sees every query
   const int k0 = kt * BN;
   const int key = k0 + 32 * w + r32;
   const int wk_lo = k0 + 32 * w;
@@ -352,7 +352,7 @@ template <int D, bool CAUSAL>
 __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dq_bf16_kernel(
     const u16* __restrict__ Q, const u16* __restrict__ K, const u16* __restrict__ V,
     const u16* __restrict__ dO, const float* __restrict__ L2, const float* __restrict__ NDelta,
-    u16* __restrict__ dQ, int Lq, int Lk, int BH, int nqt, int group, float sl2, float scale) {
+    u16* __restrict__ dQ, int Lq, int Lk, int BH, int nqt, int order, float sl2, float scale) {
   using Tile = SwzTile<D>;
   constexpr int NW = bwd_nw(D), BM = 32 * NW, BN = DQ_BN, S = kBwdStages;
   constexpr int NC = D / 16, ND = D / 32;
@@ -365,7 +365,7 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dq_bf1
 
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63, g = l >> 5, r32 = l & 31;
   int qt, bh;
-  map_tile(blockIdx.x, nqt, BH, group, qt, bh, CAUSAL);
+  map_tile(blockIdx.x, nqt, BH, order, qt, bh, CAUSAL);
   const int q0 = qt * BM;
   const int qrow = q0 + 32 * w + r32;
   const int wq_lo = q0 + 32 * w, wq_hi = wq_lo + 31;
@@ -509,7 +509,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_pipe_kernel(
     const u16* __restrict__ Q, const u16* __restrict__ K, const u16* __restrict__ V,
     const u16* __restrict__ O, const u16* __restrict__ dO, const float* __restrict__ LSE,
     float* __restrict__ L2, float* __restrict__ NDelta, u16* __restrict__ dQ, int Lq, int Lk, int BH, int nqt,
-    int group, float sl2, float scale) {
+    int order, float sl2, float scale) {
   using Tile = SwzTile<D>;
   constexpr int NW = 4, BM = 32 * NW, BN = DQP_BN, S = DQP_STAGES;
   constexpr int NC = D / 16, ND = D / 32;
@@ -522,7 +522,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_pipe_kernel(
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l = threadIdx.x & 63, g = l >> 5, r32 = l & 31;
   int qt, bh;
-  map_tile(blockIdx.x, nqt, BH, group, qt, bh, CAUSAL);
+  map_tile(blockIdx.x, nqt, BH, order, qt, bh, CAUSAL);
   const int q0 = qt * BM, wq0 = q0 + 32 * w, qrow = wq0 + r32;
   const int64_t qbase = (int64_t)bh * Lq * D;
   const int64_t kbase = (int64_t)bh * Lk * D;
@@ -727,7 +727,8 @@ static int launch_bwd(const T* q, const T* k, const T* v, const T* o, const floa
     const int64_t nqp = (Lq + 127) / 128;
     if (!grid_fits(nkt * BH, 64 * NW) || !grid_fits(nqp * BH, 256))
       return fail(TT_ERR_ARG, "attention backward: grid too large");
-    const int gp = pick_group(BH, nqp, 32 * 2), gk = pick_group(BH, nkt, 32 * 8 / NW);
+    constexpr int LD = attention_light_div(CAUSAL, D);
+    const int gp = tile_order(BH, nqp, 32 * 2, LD), gk = tile_order(BH, nkt, 32 * 8 / NW, LD);
     hipLaunchKernelGGL((attn_bwd_dq_pipe_kernel<D, CAUSAL>), dim3((unsigned)(nqp * BH)), dim3(256), 0, st, q, k, v, o,
                        dout, lse, l2, delta, dq, (int)Lq, (int)Lk, (int)BH, (int)nqp, gp, sl2, scale);
     TT_LAUNCHED("attention backward dQ launch", st);
@@ -753,7 +754,8 @@ static int launch_bwd(const T* q, const T* k, const T* v, const T* o, const floa
       if (!grid_fits(nkt * BH, 64 * NW) || !grid_fits(nqt * BH, 64 * NW))
         return fail(TT_ERR_ARG, "attention backward: grid too large");
       // heads in flight per XCD: tiles for the resident workgroups of its 32 CUs
-      const int gk = pick_group(BH, nkt, 32 * 8 / NW), gq = pick_group(BH, nqt, 32 * 8 / NW);
+      constexpr int LD = attention_light_div(CAUSAL, D);
+      const int gk = tile_order(BH, nkt, 32 * 8 / NW, LD), gq = tile_order(BH, nqt, 32 * 8 / NW, LD);
       hipLaunchKernelGGL((attn_bwd_dkdv_bf16_kernel<D, CAUSAL>), dim3((unsigned)(nkt * BH)), dim3(64 * NW), 0, st, q,
                          k, v, dout, l2, delta, dk, dv, (int)Lq, (int)Lk, (int)BH, (int)nkt, gk, sl2, scale);
       TT_LAUNCHED("attention backward dK/dV launch", st);

@@ -37,7 +37,7 @@ constexpr int FWD_F32_BM = 128;  // queries per workgroup of the fp32 kernel
 template <int D, bool CAUSAL>
 __global__ __launch_bounds__(64 * fwd_nw(D), 8 / fwd_nw(D)) void attn_fwd_bf16_kernel(
     const u16* __restrict__ Q, const u16* __restrict__ K, const u16* __restrict__ V,
-    u16* __restrict__ O, float* __restrict__ LSE, int Lq, int Lk, int BH, int nqt, int group,
+    u16* __restrict__ O, float* __restrict__ LSE, int Lq, int Lk, int BH, int nqt, int order,
     float sl2) {
   using Tile = SwzTile<D>;
   constexpr int NW = fwd_nw(D), BM = 32 * NW, BN = FWD_BN, S = kStages;
@@ -52,7 +52,7 @@ __global__ __launch_bounds__(64 * fwd_nw(D), 8 / fwd_nw(D)) void attn_fwd_bf16_k
 
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63, g = l >> 5, r32 = l & 31;
   int qt, bh;
-  map_tile(blockIdx.x, nqt, BH, group, qt, bh, CAUSAL);
+  map_tile(blockIdx.x, nqt, BH, order, qt, bh, CAUSAL);
   const int q0 = qt * BM;
   const int qrow = q0 + 32 * w + r32;
   const int64_t qbase = (int64_t)bh * Lq * D;
@@ -247,7 +247,7 @@ constexpr int FWDP_NW = 4;
 template <int D, bool CAUSAL, int NW>
 __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fwd_bf16_pipe_kernel(
     const u16* __restrict__ Q, const u16* __restrict__ K, const u16* __restrict__ V,
-    u16* __restrict__ O, float* __restrict__ LSE, int Lq, int Lk, int BH, int nqt, int group,
+    u16* __restrict__ O, float* __restrict__ LSE, int Lq, int Lk, int BH, int nqt, int order,
     float sl2) {
   using Tile = SwzTile<D>;
   constexpr int BM = 32 * NW, BN = 64;
@@ -261,7 +261,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fwd_bf16_pipe_kernel(
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l = threadIdx.x & 63, g = l >> 5, r32 = l & 31;
   int qt, bh;
-  map_tile(blockIdx.x, nqt, BH, group, qt, bh, CAUSAL);
+  map_tile(blockIdx.x, nqt, BH, order, qt, bh, CAUSAL);
   const int q0 = qt * BM, wq0 = q0 + 32 * w, qrow = wq0 + r32;
   const int64_t qbase = (int64_t)bh * Lq * D;
   const int64_t kbase = (int64_t)bh * Lk * D;
@@ -542,7 +542,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fwd_bf16_pipe_kernel(
 template <int D, bool CAUSAL>
 __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void attn_fwd_f32_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
-    float* __restrict__ O, float* __restrict__ LSE, int Lq, int Lk, int BH, int nqt, int group,
+    float* __restrict__ O, float* __restrict__ LSE, int Lq, int Lk, int BH, int nqt, int order,
     float sl2, int nsplit, float* __restrict__ part) {
   constexpr int BM = FWD_F32_BM, BN = FWD_BN;
   constexpr int NC = D / 2;   // k-steps of the d contraction (2 per MFMA)
@@ -563,7 +563,7 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void attn_fwd_f32_kernel(
   const int ntq = nqt * BH;
   const int split = blockIdx.x / ntq;
   int qt, bh;
-  map_tile(blockIdx.x - split * ntq, nqt, BH, group, qt, bh, CAUSAL);
+  map_tile(blockIdx.x - split * ntq, nqt, BH, order, qt, bh, CAUSAL);
   const int q0 = qt * BM;
   const int qrow = q0 + 32 * w + r32;
   const int64_t qbase = (int64_t)bh * Lq * D;
@@ -749,16 +749,16 @@ __global__ __launch_bounds__(256) void attn_fwd_f32_combine_kernel(const float* 
 }
 
 template <typename T, typename KernelPtr>
-static int launch_fwd(KernelPtr kern, int bm, int threads, int wg_per_cu, const T* q, const T* k, const T* v,
-                      T* o, float* lse, int64_t BH, int64_t Lq, int64_t Lk, float scale, hipStream_t s) {
+static int launch_fwd(KernelPtr kern, int bm, int threads, int wg_per_cu, int light_div, const T* q, const T* k,
+                      const T* v, T* o, float* lse, int64_t BH, int64_t Lq, int64_t Lk, float scale, hipStream_t s) {
   const int64_t nqt = (Lq + bm - 1) / bm;
   const int64_t nblk = nqt * BH;
   if (!grid_fits(nblk, threads)) return fail(TT_ERR_ARG, "attention forward: grid too large");
   // heads in flight per XCD: enough tiles for the resident workgroups of its
   // 32 CUs
-  const int group = pick_group(BH, nqt, 32 * wg_per_cu);
+  const int order = tile_order(BH, nqt, 32 * wg_per_cu, light_div);
   hipLaunchKernelGGL(kern, dim3((unsigned)nblk), dim3(threads), 0, s, q, k, v, o, lse, (int)Lq, (int)Lk,
-                     (int)BH, (int)nqt, group, scale * kLog2e);
+                     (int)BH, (int)nqt, order, scale * kLog2e);
   TT_LAUNCHED("attention forward launch", s);
   return ok();
 }
@@ -769,12 +769,12 @@ static int fwd_bf16(const u16* q, const u16* k, const u16* v, u16* o, float* lse
   if constexpr (D >= 64) {
     // two waves per SIMD: two FWDP_NW-wave workgroups per CU
     constexpr int NW = FWDP_NW;
-    return launch_fwd(attn_fwd_bf16_pipe_kernel<D, CAUSAL, NW>, 32 * NW, 64 * NW, 8 / NW, q, k, v, o, lse, BH, Lq,
-                      Lk, scale, st);
+    return launch_fwd(attn_fwd_bf16_pipe_kernel<D, CAUSAL, NW>, 32 * NW, 64 * NW, 8 / NW,
+                      attention_light_div(CAUSAL, D), q, k, v, o, lse, BH, Lq, Lk, scale, st);
   } else {
     constexpr int NW = fwd_nw(D);
-    return launch_fwd(attn_fwd_bf16_kernel<D, CAUSAL>, 32 * NW, 64 * NW, 8 / NW, q, k, v, o, lse, BH, Lq, Lk,
-                      scale, st);
+    return launch_fwd(attn_fwd_bf16_kernel<D, CAUSAL>, 32 * NW, 64 * NW, 8 / NW, attention_light_div(CAUSAL, D), q,
+                      k, v, o, lse, BH, Lq, Lk, scale, st);
   }
 }
 
@@ -792,11 +792,11 @@ static int fwd_f32(const float* q, const float* k, const float* v, float* o, flo
   if (nsplit > ktiles) nsplit = ktiles;
   if (nsplit < 1) nsplit = 1;
   if (!grid_fits(ntq * nsplit, 256)) return fail(TT_ERR_ARG, "attention forward: grid too large");
-  const int group = pick_group(BH, nqt, 32 * wg_per_cu);
+  const int order = tile_order(BH, nqt, 32 * wg_per_cu, attention_light_div(CAUSAL, D));
   const float sl2 = scale * kLog2e;
   if (nsplit == 1) {
     hipLaunchKernelGGL((attn_fwd_f32_kernel<D, CAUSAL>), dim3((unsigned)ntq), dim3(256), 0, st, q, k, v, o, lse,
-                       (int)Lq, (int)Lk, (int)BH, (int)nqt, group, sl2, 1, nullptr);
+                       (int)Lq, (int)Lk, (int)BH, (int)nqt, order, sl2, 1, nullptr);
     TT_LAUNCHED("attention forward launch", st);
     return ok();
   }
@@ -807,7 +807,7 @@ static int fwd_f32(const float* q, const float* k, const float* v, float* o, flo
   if (rc) return rc;
   float* part = (float*)ws;
   hipLaunchKernelGGL((attn_fwd_f32_kernel<D, CAUSAL>), dim3((unsigned)(ntq * nsplit)), dim3(256), 0, st, q, k, v,
-                     o, lse, (int)Lq, (int)Lk, (int)BH, (int)nqt, group, sl2, (int)nsplit, part);
+                     o, lse, (int)Lq, (int)Lk, (int)BH, (int)nqt, order, sl2, (int)nsplit, part);
   TT_LAUNCHED("attention forward split launch", st);
   constexpr int RPB = 256 / (D / 4);  // rows per combine workgroup
   hipLaunchKernelGGL((attn_fwd_f32_combine_kernel<D>), dim3((unsigned)((rows + RPB - 1) / RPB)), dim3(256), 0, st,

@@ -14,20 +14,33 @@ namespace tt {
 
 // MI355X dispatches consecutive workgroup ids round-robin over its 8 XCDs,
 // each with a private L2.  When the head count is a multiple of 8 the tiles
-// of head bh all run on XCD bh % 8 and each XCD works through `group` heads
-// at a time, so the K/V (or Q/dO) of the heads in flight stay in that L2.
-// Inside a group the tile rank runs from the most expensive causal tile
-// (the last one) to the cheapest, which evens out the tail.
-__device__ __forceinline__ void map_tile(int id, int ntile, int BH, int group, int& tile, int& bh,
+// of head bh all run on XCD bh % 8, and each XCD works through its heads in
+// two phases:
+//   1. heavy ranks (0 .. ntile - light - 1): `group` heads at a time, so the
+//      K/V (or Q/dO) of the heads in flight stay in that L2; inside a group
+//      the tile rank runs from the most expensive causal tile to cheaper ones;
+//   2. the `light` cheapest ranks of every head of the XCD, heaviest first.
+// Holding the short tiles of every head back to the end lets the XCD's
+// workgroup slots finish together instead of waiting on the heavy tiles of
+// the last head group (short tiles read little, so the lost L2 grouping
+// costs little there).  `order` packs group | light << 16 (tile_order).
+__host__ __device__ __forceinline__ void map_tile(int id, int ntile, int BH, int order, int& tile, int& bh,
                                          bool heavy_last) {
+  const int group = order & 0xffff, light = order >> 16;
   int rank;
   if ((BH & 7) == 0 && group > 0) {
-    int xcd = id & 7, t = id >> 3;
-    int per = group * ntile;
-    int gi = t / per, r = t - gi * per;
-    rank = r / group;
-    int hg = r - rank * group;
-    bh = xcd + 8 * (gi * group + hg);
+    const int xcd = id & 7, t = id >> 3, hx = BH >> 3;
+    const int nh = ntile - light, heavy = hx * nh;
+    if (t < heavy) {
+      const int per = group * nh;
+      const int gi = t / per, r = t - gi * per;
+      rank = r / group;
+      bh = xcd + 8 * (gi * group + (r - rank * group));
+    } else {
+      const int u = t - heavy;
+      rank = nh + u / hx;
+      bh = xcd + 8 * (u - (rank - nh) * hx);
+    }
   } else {
     rank = id / BH;
     bh = id - rank * BH;
@@ -47,6 +60,25 @@ inline int pick_group(int64_t BH, int64_t ntile, int64_t target) {
     if (per_xcd % gsz == 0 && gsz <= want) best = gsz;
   return (int)best;
 }
+
+// map_tile's `order` argument: the head group of pick_group and the
+// ntile / light_div cheapest ranks held back to a final phase (light_div = 0:
+// none; causal launches only, whose tiles differ in cost).  Measured on the
+// MI355X with light_div = 2: the causal d = 64 kernels 3-6 % faster at
+// L = 2048-8192 and the [16,16,1024,64] step 3 % faster; at d = 128 the
+// forward was 2 % slower (its light phase keeps the K/V of every head of the
+// XCD in flight, several times the L2) and the [4,32,4096,128] step no faster
+// (dQ -1.5 %, the dK/dV kernel after it slower), so d = 128 keeps the plain
+// grouped order (attention_light_div).
+inline int tile_order(int64_t BH, int64_t ntile, int64_t target, int light_div) {
+  const int group = pick_group(BH, ntile, target);
+  int64_t light = (light_div > 0 && group > 0) ? ntile / light_div : 0;
+  if (light > 0x7fff) light = 0x7fff;  // any count <= ntile is a valid order
+  return group | (int)(light << 16);
+}
+
+// light_div of the attention launches at head size d.
+constexpr int attention_light_div(bool causal, int d) { return causal && d <= 64 ? 2 : 0; }
 
 inline int check_attn_shape(const char* fn, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t d,
                             int causal) {
