@@ -670,15 +670,19 @@ def main(argv=None):
         return 0
 
     if args.only == "seqsweep":
-        # the c5 step (causal, bf16, H = 32, d = 128) at other sequence lengths, B * L = 16384 tokens
+        # the c5 step (causal, bf16, H = 32, d = 128) and the c3 step (H = 16, d = 64) at other sequence
+        # lengths, with the tokens per step of each (B * L = 16384) held fixed
         cases = []
-        for i, L in enumerate((1024, 2048, 4096, 8192, 16384)):
-            cfg = GpuConfig(50 + i, (C5["B"] * C5["L"]) // L, C5["H"], L, L, C5["d"], "bf16", True, True)
-            ms = run_config(T, cfg, args.steps, args.warmup)
-            tf = config_flops(cfg) / (ms * 1e-3) / 1e12
-            cases.append({"workload": f"causal fwd+bwd bf16 B={cfg.B} H={cfg.H} L={L} d={cfg.d}", "ms": ms,
-                          "value": tf, "unit": "TFLOP/s", "frac_of_peak": tf / PEAK_BF16_TFLOPS})
-            print(f"seqsweep L={L}: {ms:.4f} ms, {tf:.1f} TFLOP/s", file=sys.stderr, flush=True)
+        c3 = GPU_CONFIGS[3]
+        fams = ((C5["B"], C5["H"], C5["L"], C5["d"], 1.0), (c3.B, c3.H, c3.Lq, c3.d, c3.qkv_scale))
+        for fam, (B0, H, L0, d, qs) in enumerate(fams):
+            for i, L in enumerate((1024, 2048, 4096, 8192, 16384)):
+                cfg = GpuConfig(50 + 10 * fam + i, (B0 * L0) // L, H, L, L, d, "bf16", True, True, qs)
+                ms = run_config(T, cfg, args.steps, args.warmup)
+                tf = config_flops(cfg) / (ms * 1e-3) / 1e12
+                cases.append({"workload": f"causal fwd+bwd bf16 B={cfg.B} H={cfg.H} L={L} d={cfg.d}", "ms": ms,
+                              "value": tf, "unit": "TFLOP/s", "frac_of_peak": tf / PEAK_BF16_TFLOPS})
+                print(f"seqsweep d={d} L={L}: {ms:.4f} ms, {tf:.1f} TFLOP/s", file=sys.stderr, flush=True)
         print(json.dumps({"metric": "attn fwd+bwd TFLOP/s by sequence length (same tokens per step)",
                           "steps": args.steps, "warmup": args.warmup, "cases": cases}), flush=True)
         return 0
