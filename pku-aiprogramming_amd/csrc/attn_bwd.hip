@@ -671,7 +671,34 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_pipe_kernel(
     sdp(std::integral_constant<int, (B + 1) % 4>{}, sn, pn);
     dsq(b_tag, sc, pc, BN * n, std::false_type{});
   };
+  // Steady state without branches: while every barrier of a group of four
+  // issues a next tile that lies wholly inside Lk, barrier n always leaves
+  // exactly one tile (n + 2) in flight and loads tile n + S - 1 unclamped.
+  // (The scalar code of the general barrier -- its wait count chosen at run
+  // time, the issue test and the clamp test -- put six branches into every
+  // block.)
+  auto it_full = [&](int n, auto b_tag, f32x16& sc, f32x16& pc, f32x16& sn, f32x16& pn)
+                     __attribute__((always_inline)) {
+    constexpr int B = decltype(b_tag)::value;
+    wait_vmem_le<(S - 3) * PER>();
+    __syncthreads();
+    u16* dst = smem + 2 * ((B + S - 1) % S) * TE;  // tile n + S - 1 goes where tile n - 1 was
+    dma.issue_full(K + kbase, BN * (n + S - 1), dst);
+    dma.issue_full(V + kbase, BN * (n + S - 1), dst + TE);
+    ++issued;
+    __builtin_amdgcn_iglp_opt(2);
+    sdp(std::integral_constant<int, (B + 1) % 4>{}, sn, pn);
+    dsq(b_tag, sc, pc, BN * n, std::false_type{});
+  };
+  static_assert(S == 4, "the unrolled loops follow the ring depth");
+  const int nfull = min(ntiles, Lk / BN);  // tiles that lie wholly inside Lk
   int n = 0;
+  for (; n + 4 <= last && n + 3 + S <= nfull; n += 4) {
+    it_full(n, B0{}, sA, pA, sB, pB);
+    it_full(n + 1, B1{}, sB, pB, sA, pA);
+    it_full(n + 2, B2{}, sA, pA, sB, pB);
+    it_full(n + 3, B3{}, sB, pB, sA, pA);
+  }
   for (; n + 4 <= last; n += 4) {
     it(n, B0{}, sA, pA, sB, pB);
     it(n + 1, B1{}, sB, pB, sA, pA);

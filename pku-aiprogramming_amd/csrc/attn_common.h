@@ -298,6 +298,15 @@ struct TileDma {
     const int row = min(r0 + i * kStep, rmax - 1 - row0);
     glds16(src + (int64_t)row0 * D, 2u * (uint32_t)(row * D + 8 * ch), lds_addr(dst) + 1024u * (uint32_t)(w + NW * i));
   }
+  // Issue the loads of rows [row0, row0 + ROWS) of `src`, all of which lie
+  // inside the matrix, into the tile at `dst` (no bounds test).
+  __device__ __forceinline__ void issue_full(const u16* src, int row0, const u16* dst) const {
+    const u16* base = src + (int64_t)row0 * D;
+    const uint32_t lds = lds_addr(dst) + 1024u * (uint32_t)w;
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i)
+      glds16(base + (int64_t)D * kStep * (i - i % kPh), voff[i % kPh], lds + 1024u * NW * i);
+  }
   // Issue the loads of rows [row0, row0 + ROWS) of `src` into the tile at
   // `dst`.  Requires 0 <= row0 < rmax; rows >= rmax read row rmax - 1 instead
   // (callers mask them).  Completion: a vmcnt wait, then a barrier.
