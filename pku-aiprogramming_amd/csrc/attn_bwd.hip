@@ -91,6 +91,11 @@ __global__ __launch_bounds__(256) void attn_bwd_delta_kernel(const T* __restrict
 }
 
 // ------------------------------------------------------------------ bf16 dK, dV
+// At d = 64 the compiler fits this kernel in 166-168 VGPRs, which lets three
+// workgroups share a CU (8 % faster than two); a change that needs more
+// registers silently drops it to two.  Stating the three-workgroup bound
+// instead produced other code and was 0-1 % slower; a variant with a second,
+// branch-free copy of the loop needed 248 VGPRs (152 spilled under the bound).
 template <int D, bool CAUSAL>
 __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_bf16_kernel(
     const u16* __restrict__ Q, const u16* __restrict__ K, const u16* __restrict__ V,
