@@ -664,15 +664,19 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_pipe_kernel(
   using B1 = std::integral_constant<int, 1>;
   using B2 = std::integral_constant<int, 2>;
   using B3 = std::integral_constant<int, 3>;
+  // LLVM's interleave strategy for the scheduling region of each iteration:
+  // at d = 128 its single-wave MFMA / LDS strategy (1), at d = 64 the small-GEMM
+  // one (0).  Alternating builds on one box: c5 dQ 0.723 ms with (1) against 0.740
+  // with the MFMA / exponential strategy (2) used before and 0.742 with (0); d = 64,
+  // L = 4096 dQ 0.197 ms with (0) against 0.204 with (1) or (2).
+  constexpr int kDqIglp = D >= 128 ? 1 : 0;
   f32x16 sA, pA, sB, pB;
   sdp(B0{}, sA, pA);
   // iteration n with a next block (n < last): buffer n % 4 = B
   auto it = [&](int n, auto b_tag, f32x16& sc, f32x16& pc, f32x16& sn, f32x16& pn) __attribute__((always_inline)) {
     constexpr int B = decltype(b_tag)::value;
     barrier_n(n);
-    // LLVM's MFMA / exponential interleave strategy for the scheduling
-    // region of this iteration (2.5 % fewer cycles at d = 128)
-    __builtin_amdgcn_iglp_opt(2);
+    iglp<kDqIglp>();
     sdp(std::integral_constant<int, (B + 1) % 4>{}, sn, pn);
     dsq(b_tag, sc, pc, BN * n, std::false_type{});
   };
@@ -691,7 +695,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_pipe_kernel(
     dma.issue_full(K + kbase, BN * (n + S - 1), dst);
     dma.issue_full(V + kbase, BN * (n + S - 1), dst + TE);
     ++issued;
-    __builtin_amdgcn_iglp_opt(2);
+    iglp<kDqIglp>();
     sdp(std::integral_constant<int, (B + 1) % 4>{}, sn, pn);
     dsq(b_tag, sc, pc, BN * n, std::false_type{});
   };

@@ -133,6 +133,13 @@ __device__ __forceinline__ bf16x8 lds_read_tr16x2(const u16* p0, const u16* p1) 
 
 __device__ __forceinline__ bool wave_any(bool p) { return __any(p); }
 
+// __builtin_amdgcn_iglp_opt with a template-chosen strategy (the builtin takes
+// a constant).
+template <int K>
+__device__ __forceinline__ void iglp() {
+  __builtin_amdgcn_iglp_opt(K);
+}
+
 // Redefines x in place with no instruction, so loop-invariant code motion
 // cannot hoist (x + constant) out of a loop into a second register: the
 // constant then folds into the memory instruction's offset field.
