@@ -65,7 +65,8 @@ inline int pick_group(int64_t BH, int64_t ntile, int64_t target) {
 // ntile / light_div cheapest ranks held back to a final phase (light_div = 0:
 // none; causal launches only, whose tiles differ in cost).  Measured on the
 // MI355X with light_div = 2: the causal d = 64 kernels 3-6 % faster at
-// L = 2048-8192 and the [16,16,1024,64] step 3 % faster; at d = 128 the
+// L = 2048-8192, the [16,16,1024,64] step within +-3 % (its dK/dV kernel
+// 2 % faster, the forward and dQ 1 % slower); at d = 128 the
 // forward was 2 % slower (its light phase keeps the K/V of every head of the
 // XCD in flight, several times the L2) and the [4,32,4096,128] step no faster
 // (dQ -1.5 %, the dK/dV kernel after it slower), so d = 128 keeps the plain
