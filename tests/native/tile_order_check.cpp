@@ -1,5 +1,6 @@
 // Host-side check of the workgroup -> (tile, head) mapping of attn_tiles.h
-// (map_tile / tile_order), built with hipcc for the host only by
+// (map_tile / tile_order) and of the launch-size guard grid_fits
+// (tt_internal.h), built with hipcc for the host only by
 // tests/test_tile_order.py; no GPU is used.  For every shape below the
 // mapping must be a bijection from workgroup ids onto (tile, head) pairs,
 // keep every head on XCD bh % 8 when the head count is a multiple of 8, and
@@ -68,6 +69,12 @@ int main() {
     CHECK((order >> 16) == 0x7fff && (order & 0xffff) == 1, "order %#x", order);
     check(8, 70000, 64, 2, true);
   }
+  // launch-size guard: at most 2^32 - 1 work-items per one-dimensional launch
+  CHECK(tt::grid_fits(0, 256) && tt::grid_fits(1, 256), "small grids");
+  CHECK(tt::grid_fits(16777215, 256) && !tt::grid_fits(16777216, 256), "256-thread limit");
+  CHECK(tt::grid_fits(4194303, 1024) && !tt::grid_fits(4194304, 1024), "1024-thread limit");
+  CHECK(tt::grid_fits(4294967295LL, 1) && !tt::grid_fits(4294967296LL, 1), "1-thread limit");
+  CHECK(!tt::grid_fits(-1, 256) && !tt::grid_fits(int64_t(1) << 40, 64), "negative and huge grids");
   if (g_failures) {
     std::fprintf(stderr, "%d check(s) failed\n", g_failures);
     return 1;
