@@ -392,6 +392,7 @@ int gemm_launch(const char* fn, int transa, int transb, int64_t m, int64_t n, in
   constexpr int GN = GemmT<T>::GN;
   const int64_t gx = (n + GN - 1) / GN, gy = (m + GM - 1) / GM;
   if (gy > 65535) return fail(TT_ERR_ARG, std::string(fn) + ": m too large");
+  if (!grid_fits(gx, 256)) return fail(TT_ERR_ARG, std::string(fn) + ": n too large");
   int rc = ensure_init();
   if (rc) return rc;
   hipStream_t s = stream_or_default(stream);
