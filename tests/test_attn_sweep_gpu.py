@@ -185,3 +185,48 @@ def test_dominant_key(capi, dtype):
     rq, rk, rv = orc.attn_bwd_f64(x["q"], x["k"], x["v"], x["do"], scale, False)
     for n, a, r in (("O", o, o_ref), ("LSE", lse, l_ref), ("dQ", dq, rq), ("dK", dk, rk), ("dV", dv, rv)):
         _check(n, a, r, TOL[dtype])
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("causal", [False, True])
+def test_huge_logits(capi, dtype, causal):
+    """Inputs of scale 10 (scores up to about +-1000, log2-domain jumps of
+    hundreds): rows are one-hot up to rounding and the running max moves by
+    far more than the forward's lazy-rescale threshold within a row; against
+    the oracle.  (At scale 20, scores near +-3200, fp32 rounding of the score
+    sums alone perturbs the weights by ~2e-4: the fp32 kernels measured
+    1.4e-4 against float64 there, and the reference's own fp32 op chain
+    8e-5.)"""
+    d, L = 64, 300
+    x = _inputs(1, 2, L, L, d, 10.0, dtype, 53 + int(causal))
+    scale = float(np.float32(1.0 / math.sqrt(d)))
+    o, lse, dq, dk, dv = _fwd_bwd(capi, x, dtype, scale, causal)
+    o_ref, l_ref = orc.attn_fwd_f64(x["q"], x["k"], x["v"], scale, causal)
+    rq, rk, rv = orc.attn_bwd_f64(x["q"], x["k"], x["v"], x["do"], scale, causal)
+    assert np.isfinite(o).all() and np.isfinite(dq).all() and np.isfinite(dk).all() and np.isfinite(dv).all()
+    for n, a, r in (("O", o, o_ref), ("LSE", lse, l_ref), ("dQ", dq, rq), ("dK", dk, rk), ("dV", dv, rv)):
+        _check(n, a, r, TOL[dtype])
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("d", [64, 128])
+def test_nan_in_one_query_row_stays_where_the_oracle_puts_it(capi, dtype, d):
+    """A NaN in one query row (no mask): that row's O, LSE and dQ are NaN, so
+    are the dK and dV rows of every key (through the row's dS and P), and
+    every other value matches the oracle -- the positions the reference's op
+    chain gives (NaN propagates through max, exp and the products).  Under a
+    causal mask the reference also turns the row's masked weights into NaN
+    (exp(-inf - NaN)) and so every key's dK / dV; these kernels never touch
+    the key tiles wholly past a row's diagonal, whose dK / dV stay finite."""
+    L, bad = 200, 137
+    x = _inputs(1, 2, L, L, d, 1.0, dtype, 61 + d)
+    x["q"][0, 1, bad, 5] = np.nan
+    scale = float(np.float32(1.0 / math.sqrt(d)))
+    for causal in (False,):
+        o, lse, dq, dk, dv = _fwd_bwd(capi, x, dtype, scale, causal)
+        o_ref, l_ref = orc.attn_fwd_f64(x["q"], x["k"], x["v"], scale, causal)
+        rq, rk, rv = orc.attn_bwd_f64(x["q"], x["k"], x["v"], x["do"], scale, causal)
+        for n, a, r in (("O", o, o_ref), ("LSE", lse, l_ref), ("dQ", dq, rq), ("dK", dk, rk), ("dV", dv, rv)):
+            nan_ref = np.isnan(r)
+            assert nan_ref.any() and (np.isnan(a) == nan_ref).all(), f"{n}: NaN positions differ (causal={causal})"
+            _check(f"{n} (finite part, causal={causal})", np.where(nan_ref, 0, a), np.where(nan_ref, 0, r), TOL[dtype])
