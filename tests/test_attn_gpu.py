@@ -393,38 +393,43 @@ def test_ragged_shapes(capi, dtype, shape):
     _check("dV", dv, rv, tol)
 
 
-# Causal launches over a head count that is a multiple of 8, where the tile
-# mapping keeps every head on one XCD (id % 8) and, at d <= 64, holds each
-# head's cheapest half of the tiles back to a final phase: odd, ragged and
-# single-tile counts per head, both dtypes, every head against the oracle.
+# Launches over a head count that is a multiple of 8, where the tile mapping
+# keeps every head on one XCD (id % 8) and, for causal launches at d <= 64,
+# holds each head's cheapest half of the tiles back to a final phase: odd,
+# ragged and single-tile counts per head, both dtypes, every head against the
+# oracle; non-causal ones keep the plain head groups.
 XCD_SHAPES = [
-    # (B, H, L, d, dtype)
-    (1, 8, 300, 64, "bf16"),     # 3 query tiles per head, one held back
-    (2, 8, 1000, 64, "bf16"),    # 8 query tiles, the last one ragged
-    (1, 8, 96, 64, "bf16"),      # one query tile: nothing held back
-    (1, 16, 129, 32, "bf16"),    # the d = 32 kernels
-    (1, 8, 2048, 64, "bf16"),    # 16 query tiles
-    (1, 8, 513, 64, "f32"),      # the fp32 kernels
-    (3, 8, 700, 128, "bf16"),    # d = 128: head groups only
+    # (B, H, Lq, Lk, d, dtype, causal)
+    (1, 8, 300, 300, 64, "bf16", True),      # 3 query tiles per head, one held back
+    (2, 8, 1000, 1000, 64, "bf16", True),    # 8 query tiles, the last one ragged
+    (1, 8, 96, 96, 64, "bf16", True),        # one query tile: nothing held back
+    (1, 16, 129, 129, 32, "bf16", True),     # the d = 32 kernels
+    (1, 8, 2048, 2048, 64, "bf16", True),    # 16 query tiles
+    (1, 8, 513, 513, 64, "f32", True),       # the fp32 kernels
+    (3, 8, 700, 700, 128, "bf16", True),     # d = 128: head groups only
+    (2, 8, 700, 333, 64, "bf16", False),     # non-causal, Lq != Lk
+    (1, 16, 257, 900, 128, "bf16", False),
+    (1, 8, 300, 500, 64, "f32", False),
 ]
 
 
 @pytest.mark.parametrize("shape", XCD_SHAPES, ids=[str(s) for s in XCD_SHAPES])
-def test_causal_xcd_grouped_tile_order(capi, shape):
-    B, H, L, d, dtype = shape
-    _say(f"xcd-grouped causal {dtype} B={B} H={H} L={L} d={d}")
-    rng = np.random.default_rng(3000 + L + d + B * H)
-    x = {n: rng.standard_normal((B, H, L, d), dtype=np.float32) for n in ("q", "k", "v", "do")}
+def test_xcd_grouped_tile_order(capi, shape):
+    B, H, Lq, Lk, d, dtype, causal = shape
+    _say(f"xcd-grouped {dtype} B={B} H={H} Lq={Lq} Lk={Lk} d={d} causal={causal}")
+    rng = np.random.default_rng(3000 + Lq + Lk + d + B * H)
+    x = {n: rng.standard_normal((B, H, L, d), dtype=np.float32)
+         for n, L in (("q", Lq), ("k", Lk), ("v", Lk), ("do", Lq))}
     if dtype == "bf16":
         x = {n: orc.bf16_round(a) for n, a in x.items()}
     scale = float(np.float32(1.0 / math.sqrt(d)))
     tol = TOL[dtype]
-    b = _run_fwd(capi, x, dtype, scale, True)
-    o_ref, l_ref = orc.attn_fwd_f64(x["q"], x["k"], x["v"], scale, True)
+    b = _run_fwd(capi, x, dtype, scale, causal)
+    o_ref, l_ref = orc.attn_fwd_f64(x["q"], x["k"], x["v"], scale, causal)
     _check("O", b["o"].download(), o_ref, tol)
     _check("LSE", b["lse"].download(), l_ref, tol)
-    dq, dk, dv = _run_bwd(capi, b, x["do"], dtype, scale, True)
-    rq, rk, rv = orc.attn_bwd_f64(x["q"], x["k"], x["v"], x["do"], scale, True)
+    dq, dk, dv = _run_bwd(capi, b, x["do"], dtype, scale, causal)
+    rq, rk, rv = orc.attn_bwd_f64(x["q"], x["k"], x["v"], x["do"], scale, causal)
     # per head, so that one wrong head cannot hide behind the others' scale
     for bb in range(B):
         for hh in range(H):
