@@ -1,6 +1,7 @@
 """Seeded random sweep of the attention entry points (forward, backward,
 decode; fp32 and bf16) against the float64 oracle, beyond the fixed shapes of
-test_attn_gpu.py: random batch / head counts, lengths from 1 to 700 (ragged
+test_attn_gpu.py: random batch / head counts (16 of the cases over head
+counts that are multiples of 8), lengths from 1 to 700 or 1500 (ragged
 against every tile size, Lq != Lk when not causal), every head dim, and input
 scales from 0.25 to 4, so that the softmax ranges from nearly uniform to
 nearly one-hot (score spreads far past the forward's lazy-rescale threshold
@@ -39,22 +40,28 @@ def capi():
     return tt_capi
 
 
-def _cases(n=24, seed=2024):
+def _cases(n=24, seed=2024, heads=None, lmax=700, base=5000):
     rng = np.random.default_rng(seed)
     out = []
     for i in range(n):
         d = int(rng.choice([32, 64, 128]))
         causal = bool(rng.integers(0, 2))
-        Lq = int(rng.integers(1, 701))
-        Lk = Lq if causal else int(rng.integers(1, 701))
-        B, H = int(rng.integers(1, 4)), int(rng.integers(1, 4))
+        Lq = int(rng.integers(1, lmax + 1))
+        Lk = Lq if causal else int(rng.integers(1, lmax + 1))
+        if heads is None:
+            B, H = int(rng.integers(1, 4)), int(rng.integers(1, 4))
+        else:
+            B, H = heads[int(rng.integers(0, len(heads)))]
         sigma = float(rng.choice([0.25, 1.0, 2.0, 4.0]))
         dtype = "bf16" if i % 2 else "f32"
-        out.append((B, H, Lq, Lk, d, causal, sigma, dtype, 5000 + i))
+        out.append((B, H, Lq, Lk, d, causal, sigma, dtype, base + i))
     return out
 
 
 CASES = _cases()
+# head counts that are multiples of 8: the launches' per-XCD head groups and,
+# for causal d <= 64, the held-back cheap tiles (attn_tiles.h)
+CASES += _cases(16, seed=2025, heads=[(1, 8), (2, 8), (1, 16), (3, 8)], lmax=1500, base=6000)
 
 
 def _inputs(B, H, Lq, Lk, d, sigma, dtype, seed):
