@@ -21,12 +21,11 @@
 //   dq:   workgroup = NW waves x 32 queries (lane = query, as the forward);
 //         loops over key tiles: S^T and dP^T from K / V row reads,
 //         dQ^T += K^T dS^T from transpose reads of the same K tile.
-// bf16 at d >= 64: the dq kernel (attn_bwd_dq_pipe_kernel) runs first and
-// also writes the rows -D and LSE log2(e) the dkdv kernel reads; at d = 128
-// the dK / dV role runs one wave per SIMD with 64 keys per wave
-// (attn_bwd_w64.hip), at d = 64 the kernel below.  d = 32 runs a separate
-// row pre-pass (attn_bwd_delta_kernel), then dkdv, then dq.  fp32
-// (attn_bwd_f32.h): the pre-pass, then one launch holding both roles.
+// bf16: the dq kernel (attn_bwd_dq_pipe_kernel) runs first and also writes
+// the rows -D and LSE log2(e) the dkdv kernel reads; at d = 128 the dK / dV
+// role runs one wave per SIMD with 64 keys per wave (attn_bwd_w64.hip), at
+// d = 32 and 64 the kernel below.  fp32 (attn_bwd_f32.h): a separate row
+// pre-pass (attn_bwd_delta_kernel), then one launch holding both roles.
 // All bf16 tiles are filled by direct global->LDS loads.  Loads past the end
 // of a sequence read a clamped (valid) row and the result is masked, so the
 // inner loops carry no load guards.
@@ -47,7 +46,6 @@ namespace tt {
 // than one 8-wave workgroup with a 4-deep ring.
 constexpr int bwd_nw(int) { return 4; }
 constexpr int kBwdStages = 2;
-constexpr int DQ_BN = 64;  // keys per LDS tile of the d = 32 dQ kernel
 // Query rows per LDS tile of the d <= 64 dK/dV kernel.
 constexpr int kDkdvBQ = 64;
 
@@ -352,143 +350,7 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_b
   store_staged_rows<D>(stage + BN * D, BN, dV + kbase, k0, Lk, 64 * NW);
 }
 
-// ------------------------------------------------------------------ bf16 dQ
-template <int D, bool CAUSAL>
-__global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dq_bf16_kernel(
-    const u16* __restrict__ Q, const u16* __restrict__ K, const u16* __restrict__ V,
-    const u16* __restrict__ dO, const float* __restrict__ L2, const float* __restrict__ NDelta,
-    u16* __restrict__ dQ, int Lq, int Lk, int BH, int nqt, int order, float sl2, float scale) {
-  using Tile = SwzTile<D>;
-  constexpr int NW = bwd_nw(D), BM = 32 * NW, BN = DQ_BN, S = kBwdStages;
-  constexpr int NC = D / 16, ND = D / 32;
-  constexpr int TE = Tile::kElems(BN);
-  using Dma = TileDma<D, BN, NW>;
-  constexpr int IPT = 2 * Dma::kLoads;  // K + V loads per wave per tile
-  // rings of K / V tiles filled by direct global->LDS loads
-  __shared__ __align__(16) u16 sK[S * TE];
-  __shared__ __align__(16) u16 sV[S * TE];
-
-  const int w = threadIdx.x >> 6, l = threadIdx.x & 63, g = l >> 5, r32 = l & 31;
-  int qt, bh;
-  map_tile(blockIdx.x, nqt, BH, order, qt, bh, CAUSAL);
-  const int q0 = qt * BM;
-  const int qrow = q0 + 32 * w + r32;
-  const int wq_lo = q0 + 32 * w, wq_hi = wq_lo + 31;
-  const int64_t qbase = (int64_t)bh * Lq * D;
-  const int64_t kbase = (int64_t)bh * Lk * D;
-
-  bf16x8 qf[NC], dof[NC];
-  {
-    const int qr = min(qrow, Lq - 1);
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      qf[c] = __builtin_bit_cast(bf16x8, ldg16(Q + qbase + (int64_t)qr * D + 16 * c + 8 * g));
-      dof[c] = __builtin_bit_cast(bf16x8, ldg16(dO + qbase + (int64_t)qr * D + 16 * c + 8 * g));
-    }
-  }
-  // padding query rows (qrow >= Lq): P = 2^(s - inf) = 0
-  const float lse2 = qrow < Lq ? L2[(int64_t)bh * Lq + qrow] : INFINITY;
-  const float ndl = qrow < Lq ? NDelta[(int64_t)bh * Lq + qrow] : 0.f;
-  f32x16 adq[ND];
-#pragma unroll
-  for (int dt = 0; dt < ND; ++dt) adq[dt] = f32x16{};
-
-  const int t16 = l & 15;
-  const int trow = 4 * g + (t16 >> 2);
-  const int tcol = 16 * ((l >> 4) & 1) + 4 * (t16 & 3);
-
-  // Tile ring over key tiles; rows past Lk read row Lk - 1 and are masked.
-  const int kend = CAUSAL ? min(Lk, q0 + BM) : Lk;
-  const int ntiles = (kend + BN - 1) / BN;
-  Dma dma;
-  dma.init();
-  int issued = 0;
-  auto issue_next = [&]() {
-    if (issued < ntiles) {
-      const int b = issued % S;
-      dma.issue(K + kbase, issued * BN, Lk, sK + b * TE);
-      dma.issue(V + kbase, issued * BN, Lk, sV + b * TE);
-      ++issued;
-    }
-  };
-
-  auto tile = [&](int kb, const u16* tK, const u16* tV, auto mask_tag) {
-    constexpr bool MASK = decltype(mask_tag)::value;
-    // Operand fetches run one step ahead of the MFMAs that consume them.
-    auto kv_row = [&](const u16* tile_, int t, int c) {
-      return *reinterpret_cast<const bf16x8*>(&tile_[Tile::chunk(32 * t + r32, 2 * c + g)]);
-    };
-    auto kt_op = [&](int t, int i) {  // K^T operand of dQ^T MFMA i = h * ND + dt
-      const int r0 = 32 * t + 16 * (i / ND) + trow, col = 32 * (i % ND) + tcol;
-      return lds_read_tr16x2(&tK[Tile::at4(r0, col)], &tK[Tile::at4(r0 + 8, col)]);
-    };
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      f32x16 s = f32x16{}, dp = f32x16{};
-      bf16x8 ka[2], va[2];
-      ka[0] = kv_row(tK, t, 0);
-      va[0] = kv_row(tV, t, 0);
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        if (c + 1 < NC) {
-          ka[(c + 1) & 1] = kv_row(tK, t, c + 1);
-          va[(c + 1) & 1] = kv_row(tV, t, c + 1);
-        }
-        s = mfma_bf16_32x32x16(ka[c & 1], qf[c], s);
-        dp = mfma_bf16_32x32x16(va[c & 1], dof[c], dp);
-      }
-      bf16x8 qa[2];
-      qa[0] = kt_op(t, 0);  // in flight during the softmax
-      bf16x8 db[2];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float p = fast_exp2(fmaf(s[r], sl2, -lse2));
-        if constexpr (MASK) {
-          const int kk = kb + 32 * t + acc_row(r, g);
-          if (kk >= Lk || (CAUSAL && kk > qrow)) p = 0.f;
-        }
-        db[r >> 3][r & 7] = (__bf16)(p * (dp[r] + ndl));
-      }
-#pragma unroll
-      for (int i = 0; i < 2 * ND; ++i) {
-        if (i + 1 < 2 * ND) qa[(i + 1) & 1] = kt_op(t, i + 1);
-        adq[i % ND] = mfma_bf16_32x32x16(qa[i & 1], db[i / ND], adq[i % ND]);
-      }
-    }
-  };
-
-  int j = 0;
-  auto run = [&](int lo, int hi, auto mask_tag) {
-    for (int kb = lo; kb < hi; kb += BN, ++j) {
-      wait_vmem_tiles<IPT>(issued - 1 - j);
-      __syncthreads();
-      issue_next();
-      if (CAUSAL && kb > wq_hi) continue;
-      const int b = j % S;
-      tile(kb, sK + b * TE, sV + b * TE, mask_tag);
-    }
-  };
-  for (int s0 = 0; s0 < S - 1; ++s0) issue_next();
-  wait_vmem_le<0>();  // retire the Q / dO / LSE / D loads (see the dK/dV kernel)
-  const int kfull = CAUSAL ? min(q0, (Lk / BN) * BN) : (Lk / BN) * BN;  // unmasked tiles
-  run(0, kfull, std::false_type{});
-  run(kfull, kend, std::true_type{});
-
-  if (qrow < Lq) {
-    u16* row = dQ + qbase + (int64_t)qrow * D;
-#pragma unroll
-    for (int dt = 0; dt < ND; ++dt)
-#pragma unroll
-      for (int r = 0; r < 16; r += 4) {
-        uint2 v;
-        v.x = pack_bf16x2(adq[dt][r] * scale, adq[dt][r + 1] * scale);
-        v.y = pack_bf16x2(adq[dt][r + 2] * scale, adq[dt][r + 3] * scale);
-        *reinterpret_cast<uint2*>(row + 32 * dt + acc_row(r, g)) = v;
-      }
-  }
-}
-
-// ------------------------------------------------------------------ bf16 dQ, software-pipelined (D = 64, 128)
+// ------------------------------------------------------------------ bf16 dQ, software-pipelined (D = 32, 64, 128)
 // Workgroup = 4 waves x 32 queries (lane = query, as the forward); blocks of
 // 32 keys (a K tile and a V tile) stream through a 4-deep LDS ring filled by
 // direct global->LDS loads.  Iteration n of a wave:
@@ -756,7 +618,7 @@ static int launch_bwd(const T* q, const T* k, const T* v, const T* o, const floa
   const int64_t rows = BH * Lq;
   float* l2 = delta + rows;
   const float sl2 = scale * kLog2e;
-  if constexpr (BF && D >= 64) {
+  if constexpr (BF) {
     // dQ first: it also writes -D and LSE * log2(e) for the dK/dV kernel
     constexpr int NW = bwd_nw(D);
     const int64_t nkt = (Lk + 32 * NW - 1) / (32 * NW);
@@ -783,22 +645,8 @@ static int launch_bwd(const T* q, const T* k, const T* v, const T* o, const floa
                        l2, rows);
     TT_LAUNCHED("attention backward delta launch", st);
 
-    if constexpr (BF) {
-      constexpr int NW = bwd_nw(D);
-      const int64_t nkt = (Lk + 32 * NW - 1) / (32 * NW);
-      const int64_t nqt = (Lq + 32 * NW - 1) / (32 * NW);
-      if (!grid_fits(nkt * BH, 64 * NW) || !grid_fits(nqt * BH, 64 * NW))
-        return fail(TT_ERR_ARG, "attention backward: grid too large");
-      // heads in flight per XCD: tiles for the resident workgroups of its 32 CUs
-      constexpr int LD = attention_light_div(CAUSAL, D);
-      const int gk = tile_order(BH, nkt, 32 * 8 / NW, LD), gq = tile_order(BH, nqt, 32 * 8 / NW, LD);
-      hipLaunchKernelGGL((attn_bwd_dkdv_bf16_kernel<D, CAUSAL>), dim3((unsigned)(nkt * BH)), dim3(64 * NW), 0, st, q,
-                         k, v, dout, l2, delta, dk, dv, (int)Lq, (int)Lk, (int)BH, (int)nkt, gk, sl2, scale);
-      TT_LAUNCHED("attention backward dK/dV launch", st);
-      hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<D, CAUSAL>), dim3((unsigned)(nqt * BH)), dim3(64 * NW), 0, st, q, k,
-                         v, dout, l2, delta, dq, (int)Lq, (int)Lk, (int)BH, (int)nqt, gq, sl2, scale);
-      TT_LAUNCHED("attention backward dQ launch", st);
-    } else {
+    {
+      // fp32: dK/dV and dQ workgroups in one launch
       const int64_t nkt = (Lk + BWD_F32_BN - 1) / BWD_F32_BN;
       const int64_t nqt = (Lq + BWD_F32_BM - 1) / BWD_F32_BM;
       if (!grid_fits((nkt + nqt) * BH, 256)) return fail(TT_ERR_ARG, "attention backward: grid too large");

@@ -256,11 +256,12 @@ __device__ __forceinline__ void glds4(const void* sbase, uint32_t voff, uint32_t
 #pragma clang diagnostic pop
 
 // Direct global->LDS loader of [ROWS x D] bf16 tiles of a row-major [*, D]
-// matrix into SwzTile<D> buffers, shared by the NW waves of a workgroup.
-// Load instruction i of wave w fills the 64 consecutive 16-byte LDS slots
-// starting at slot 64 (i NW + w); each lane fetches the global chunk that
-// belongs in its slot.  One instruction covers 64 / kCPR rows, so step i
-// moves kStep = NW * 64 / kCPR rows on.  Every swizzle has a period
+// matrix into SwzTile<D> buffers, shared by the loading waves (kWaves: all NW
+// of the workgroup, or fewer for tiles smaller than one instruction per
+// wave).  Load instruction i of wave w fills the 64 consecutive 16-byte LDS
+// slots starting at slot 64 (i kWaves + w); each lane fetches the global
+// chunk that belongs in its slot.  One instruction covers 64 / kCPR rows, so
+// step i moves kStep = kWaves * 64 / kCPR rows on.  Every swizzle has a period
 // dividing 16 rows, so the lane's chunk column repeats every kPh = 16 /
 // gcd(kStep, 16) instructions: instruction i reads at byte offset
 // voff[i % kPh] + 2 D kStep (i - i % kPh), with the kPh offsets computed
@@ -268,11 +269,16 @@ __device__ __forceinline__ void glds4(const void* sbase, uint32_t voff, uint32_t
 template <int D, int ROWS, int NW>
 struct TileDma {
   static constexpr int kCPR = D / 8;
-  static_assert(ROWS * kCPR % (64 * NW) == 0, "tile must split evenly over the waves");
-  static constexpr int kStep = NW * 64 / kCPR;  // rows per load instruction of the workgroup
+  // waves that load: all NW, or the first ones when the tile holds fewer
+  // 16-byte chunks than one instruction of every wave (32-row tiles at d = 32)
+  static constexpr int kWaves = ROWS * kCPR >= 64 * NW ? NW : ROWS * kCPR / 64;
+  static_assert(kWaves >= 1 && ROWS * kCPR % (64 * kWaves) == 0, "tile must split evenly over the waves");
+  static constexpr int kStep = kWaves * 64 / kCPR;  // rows per load instruction of the workgroup
   static_assert(kStep % 16 == 0 || 16 % kStep == 0, "row step must divide or be a multiple of 16");
   static constexpr int kPh = kStep % 16 == 0 ? 1 : 16 / kStep;
-  static constexpr int kLoads = ROWS * kCPR / (64 * NW);  // load instructions per wave per tile
+  static constexpr int kLoads = ROWS * kCPR / (64 * kWaves);  // load instructions per loading wave per tile
+  // waves w >= kWaves issue nothing (w is wave-uniform)
+  __device__ __forceinline__ bool idle() const { return kWaves < NW && w >= kWaves; }
   static_assert(kLoads % kPh == 0 || kLoads < kPh, "loads must cover whole swizzle periods");
   uint32_t voff[kPh];  // this lane's byte offsets for instructions 0..kPh-1, from the tile's first row
   int w;
@@ -292,38 +298,42 @@ struct TileDma {
   // right after a barrier, the loads of every wave queue at the CU's texture
   // address unit and each wave stalls until its own are accepted.
   __device__ __forceinline__ void issue_one(const u16* src, int row0, const u16* dst, int i) const {
+    if (idle()) return;
     glds16(src + (int64_t)row0 * D + (int64_t)D * kStep * (i - i % kPh), voff[i % kPh],
-           lds_addr(dst) + 1024u * (uint32_t)(w + NW * i));
+           lds_addr(dst) + 1024u * (uint32_t)(w + kWaves * i));
   }
   // Load instruction i (0 <= i < kLoads) alone of issue(src, row0, rmax,
   // dst), always by the clamped form (no branch), for kernels that spread a
   // tile's loads over their compute.  Requires 0 <= row0 < rmax.
   __device__ __forceinline__ void issue_part_clamped(const u16* src, int row0, int rmax, const u16* dst, int i) const {
+    if (idle()) return;
     const int p0 = w * 64 + (threadIdx.x & 63);
     const int r0 = p0 / kCPR;
     const int ch = (p0 % kCPR) ^ SwzTile<D>::sw(r0 + i * kStep);
     const int row = min(r0 + i * kStep, rmax - 1 - row0);
-    glds16(src + (int64_t)row0 * D, 2u * (uint32_t)(row * D + 8 * ch), lds_addr(dst) + 1024u * (uint32_t)(w + NW * i));
+    glds16(src + (int64_t)row0 * D, 2u * (uint32_t)(row * D + 8 * ch), lds_addr(dst) + 1024u * (uint32_t)(w + kWaves * i));
   }
   // Issue the loads of rows [row0, row0 + ROWS) of `src`, all of which lie
   // inside the matrix, into the tile at `dst` (no bounds test).
   __device__ __forceinline__ void issue_full(const u16* src, int row0, const u16* dst) const {
+    if (idle()) return;
     const u16* base = src + (int64_t)row0 * D;
     const uint32_t lds = lds_addr(dst) + 1024u * (uint32_t)w;
 #pragma unroll
     for (int i = 0; i < kLoads; ++i)
-      glds16(base + (int64_t)D * kStep * (i - i % kPh), voff[i % kPh], lds + 1024u * NW * i);
+      glds16(base + (int64_t)D * kStep * (i - i % kPh), voff[i % kPh], lds + 1024u * kWaves * i);
   }
   // Issue the loads of rows [row0, row0 + ROWS) of `src` into the tile at
   // `dst`.  Requires 0 <= row0 < rmax; rows >= rmax read row rmax - 1 instead
   // (callers mask them).  Completion: a vmcnt wait, then a barrier.
   __device__ __forceinline__ void issue(const u16* src, int row0, int rmax, const u16* dst) const {
+    if (idle()) return;
     const u16* base = src + (int64_t)row0 * D;
     const uint32_t lds = lds_addr(dst) + 1024u * (uint32_t)w;
     if (row0 + ROWS <= rmax) {
 #pragma unroll
       for (int i = 0; i < kLoads; ++i)
-        glds16(base + (int64_t)D * kStep * (i - i % kPh), voff[i % kPh], lds + 1024u * NW * i);
+        glds16(base + (int64_t)D * kStep * (i - i % kPh), voff[i % kPh], lds + 1024u * kWaves * i);
     } else {
       const int p0 = w * 64 + (threadIdx.x & 63);
       const int r0 = p0 / kCPR;
@@ -332,7 +342,7 @@ struct TileDma {
         // the slot's chunk column follows the swizzle of its own (unclamped) row
         const int ch = (p0 % kCPR) ^ SwzTile<D>::sw(r0 + i * kStep);
         const int row = min(r0 + i * kStep, rmax - 1 - row0);
-        glds16(base, 2u * (uint32_t)(row * D + 8 * ch), lds + 1024u * NW * i);
+        glds16(base, 2u * (uint32_t)(row * D + 8 * ch), lds + 1024u * kWaves * i);
       }
     }
   }
