@@ -238,7 +238,9 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_b
         }
       }
       // dV^T += dO^T P and dK^T += Q^T dS over the 32 queries of this half:
-      // k-chunk h holds queries 32mt + 16h + perm16 order.
+      // element e of k-chunk h is accumulator row acc_row(8h + e, g), query
+      // 32mt + 16h + 8(e / 4) + 4g + e % 4, the order in which the transpose
+      // reads of rows trow and trow + 8 deliver the dO / Q columns.
       bf16x8 ov[2], oq[2];
       ov[0] = tr_op(kOdO - kOQ, 0);
       oq[0] = tr_op(0, 0);

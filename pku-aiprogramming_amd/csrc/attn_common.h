@@ -52,14 +52,6 @@ __device__ __forceinline__ f32x16 mfma_f32_32x32x2(float a, float b, const f32x1
 // Row of the 32x32 accumulator tile held in register r by a lane in half g.
 __device__ __forceinline__ constexpr int acc_row(int r, int g) { return 8 * (r >> 2) + 4 * g + (r & 3); }
 
-// Key order inside a 16-key k-chunk of the P^T operand.  Accumulator
-// registers 8h..8h+7 of lane half g hold keys 16h' + 8*(e/4) + 4*g + e%4, so
-// a [d][key] LDS tile stores key j at position perm16(j) (bits 2 and 3 of j
-// swapped); a lane then reads its 8 keys as one 16-byte vector.
-__device__ __forceinline__ constexpr int perm16(int j) {
-  return (j & ~12) | ((j & 4) << 1) | ((j & 8) >> 1);
-}
-
 __device__ __forceinline__ float wave_xor32(float x) { return __shfl_xor(x, 32, 64); }
 
 // Reductions over lanes l and l ^ 32 in two VALU ops, with no LDS round
@@ -377,9 +369,5 @@ __device__ __forceinline__ void load_vec_lds(const float* src, int nmax, const f
   asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
   glds4(src, 4u * (uint32_t)min(l, nmax - 1), lds_addr(dst));
 }
-
-// Wait for this wave's outstanding global loads (incl. direct-to-LDS ones):
-// s_waitcnt vmcnt(0), leaving the LDS and export counters alone.
-__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 }  // namespace tt
