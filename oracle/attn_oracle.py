@@ -229,18 +229,6 @@ def decode_split_merge_f64(q, k, v, scale: float, splits: int):
     return o, lse
 
 
-def attn_fwd_f64_heads(q, k, v, scale, causal, heads=None):
-    """Per-(b,h) float64 forward over [B,H,L,d] to bound memory; ``heads`` is
-    an optional list of (b, h) pairs."""
-    B, H = q.shape[:2]
-    heads = heads if heads is not None else [(b, h) for b in range(B) for h in range(H)]
-    o = {}
-    lse = {}
-    for b, h in heads:
-        o[(b, h)], lse[(b, h)] = attn_fwd_f64(q[b, h], k[b, h], v[b, h], scale, causal)
-    return o, lse
-
-
 # ---------------------------------------------------------------------------
 # The reference's op sequence in float32 (timed CPU baseline)
 # ---------------------------------------------------------------------------
