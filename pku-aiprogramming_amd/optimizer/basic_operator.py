@@ -24,6 +24,10 @@ from __future__ import annotations
 
 from typing import Any, Iterable, Optional, Tuple
 
+# Graph nodes made and not yet collected in this process, as the reference's
+# module counter (basic_operator.py:9, 63-65, 76-77).
+TENSOR_COUNTER = 0
+
 
 class Op:
     """An operation of the graph."""
@@ -59,7 +63,13 @@ class Value:
     cached_data: Any
     requires_grad: bool
 
+    _counted = False  # whether TENSOR_COUNTER holds this node
+
     def _setup(self, op: Optional[Op], inputs: Iterable["Value"], data, requires_grad: Optional[bool]) -> None:
+        global TENSOR_COUNTER
+        if not self._counted:
+            TENSOR_COUNTER += 1
+            self._counted = True
         self.op = op
         self.inputs = list(inputs)
         self.cached_data = data
@@ -67,6 +77,14 @@ class Value:
             requires_grad = any(x.requires_grad for x in self.inputs)
         self.requires_grad = bool(requires_grad)
         self.saved = None  # per-node state an op keeps between forward and gradient
+
+    def __del__(self):
+        global TENSOR_COUNTER
+        if self._counted:
+            try:
+                TENSOR_COUNTER -= 1
+            except TypeError:  # interpreter shutdown may have cleared the module
+                pass
 
     def realize_cached_data(self):
         if self.cached_data is None:

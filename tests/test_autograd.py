@@ -241,6 +241,22 @@ def test_make_const_unwraps_a_tensor_and_takes_requires_grad_positionally(ops):
     np.testing.assert_array_equal(g.grad.numpy(), [3.0, 3.0])
 
 
+def test_tensor_counter_counts_live_nodes(ops):
+    import gc
+
+    import basic_operator as bo
+
+    gc.collect()
+    base = bo.TENSOR_COUNTER
+    a = ops.Tensor(np.ones(3))
+    b = ops.Tensor.make_const(np.zeros(3))
+    c = a + b  # one op node
+    assert bo.TENSOR_COUNTER == base + 3
+    del a, b, c
+    gc.collect()
+    assert bo.TENSOR_COUNTER == base
+
+
 def test_causal_mask_closed_form(ops):
     m = ops.causal_mask(3, 5)
     assert m.dtype == np.float32
