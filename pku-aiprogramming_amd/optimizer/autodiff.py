@@ -2,8 +2,9 @@
 
 Same entry points and results as the reference driver
 (Task3/Tinytensor/optimizer/autodiff.py:9-61): ``find_topo_sort`` returns the
-nodes inputs-first, and ``compute_gradient_of_variables(output, out_grad)``
-leaves in every node's ``.grad`` the gradient of sum(output * out_grad).
+nodes inputs-first, ``topo_sort_dfs`` is its post-order walk helper, and
+``compute_gradient_of_variables(output, out_grad)`` leaves in every node's
+``.grad`` the gradient of sum(output * out_grad).
 
 The order is found by Kahn's algorithm on user counts instead of a recursive
 depth-first search, so graphs of any depth need no recursion limit: a node
@@ -44,6 +45,28 @@ def _users_first(outputs: List[Value]) -> List[Value]:
             if users[inp] == 0:
                 ready.append(inp)
     return order
+
+
+def topo_sort_dfs(node: Value, visited: set, topo_order: List[Value]) -> None:
+    """Post-order depth-first walk from `node` (the reference's helper of the
+    same name, autodiff.py:24-31): every node reachable from it that is not in
+    `visited` yet is added to `visited` and appended to `topo_order` after its
+    inputs, which are walked in list order.  Iterative, so a deep graph needs
+    no recursion limit."""
+    if node in visited:
+        return
+    visited.add(node)
+    stack = [(node, iter(node.inputs))]
+    while stack:
+        cur, rest = stack[-1]
+        for inp in rest:
+            if inp not in visited:
+                visited.add(inp)
+                stack.append((inp, iter(inp.inputs)))
+                break
+        else:
+            stack.pop()
+            topo_order.append(cur)
 
 
 def find_topo_sort(node_list: List[Value]) -> List[Value]:

@@ -126,6 +126,41 @@ def test_topological_order_on_a_diamond_with_repeated_inputs(ops):
     np.testing.assert_allclose(x.grad.numpy(), 3 * xv ** 2 + 8 * xv)
 
 
+def test_topo_sort_dfs_is_the_post_order_walk(ops):
+    import autodiff
+
+    def rec(node, visited, out):  # the definition: recursive post-order DFS
+        if node in visited:
+            return
+        visited.add(node)
+        for i in node.inputs:
+            rec(i, visited, out)
+        out.append(node)
+
+    x = ops.Tensor(np.array([1.0, 2.0]))
+    w = ops.Tensor(np.array([3.0, -1.0]))
+    a = x * x
+    b = x + w
+    c = a * b
+    d = c + a
+    e = d * w
+    for roots in ([e], [d, e], [b, e, a]):
+        want, got = [], []
+        vw, vg = set(), set()
+        for r in roots:
+            rec(r, vw, want)
+            autodiff.topo_sort_dfs(r, vg, got)
+        assert [id(n) for n in got] == [id(n) for n in want]
+        assert vg == vw
+    # a deep chain needs no recursion limit
+    y = x
+    for _ in range(5000):
+        y = y + 1.0
+    out = []
+    autodiff.topo_sort_dfs(y, set(), out)
+    assert len(out) == 5001 and out[0] is x and out[-1] is y
+
+
 def test_topological_order_of_several_outputs(ops):
     import autodiff
 
