@@ -255,8 +255,8 @@ def config_step(T, cfg, bufs, part="all"):
     return step
 
 
-def run_config(T, cfg, steps, warmup):
-    step = config_step(T, cfg, config_buffers(T, cfg))
+def run_config(T, cfg, steps, warmup, part="all"):
+    step = config_step(T, cfg, config_buffers(T, cfg), part)
     prewarm(T, step)
     for _ in range(warmup):
         step()
@@ -630,11 +630,12 @@ def main(argv=None):
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--only", choices=["all", "fwdbwd", "configs", "decode", "copy", "ceiling", "softmax", "gemm", "io",
-                                       "sustain", "seqsweep"],
+                                       "sustain", "seqsweep", "shapes"],
                     default="all",
                     help="run one workload only (for profiler runs; 'copy' is the 1 GiB calibration copy, "
                          "'ceiling' the library bf16 GEMM reference, 'sustain' the --sustain loop, 'seqsweep' "
-                         "the c5 step at L = 1024 .. 16384 over the same number of tokens)")
+                         "the c5 step at L = 1024 .. 16384 over the same number of tokens, 'shapes' every head "
+                         "size, causal and not, in both dtypes)")
     ap.add_argument("--sustain", default="3:all:8", metavar="CID:PART:SECONDS",
                     help="with --only sustain: config (1, 2, 3 or 5), part (all, fwd or bwd) and duration of a "
                          "loop of 200-step batches")
@@ -684,6 +685,28 @@ def main(argv=None):
                               "value": tf, "unit": "TFLOP/s", "frac_of_peak": tf / PEAK_BF16_TFLOPS})
                 print(f"seqsweep d={d} L={L}: {ms:.4f} ms, {tf:.1f} TFLOP/s", file=sys.stderr, flush=True)
         print(json.dumps({"metric": "attn fwd+bwd TFLOP/s by sequence length (same tokens per step)",
+                          "steps": args.steps, "warmup": args.warmup, "cases": cases}), flush=True)
+        return 0
+
+    if args.only == "shapes":
+        # every supported head size, causal and not: bf16 at two sequence lengths over 16384 tokens of 32
+        # heads per step, fp32 at one over 4096 tokens of 16 heads; forward alone and forward + backward
+        grid = [("bf16", 32, 16384, L, d, c) for d in (32, 64, 128) for c in (True, False) for L in (1024, 4096)]
+        grid += [("f32", 16, 4096, 2048, d, c) for d in (32, 64, 128) for c in (True, False)]
+        cases = []
+        for i, (dt, H, tokens, L, d, causal) in enumerate(grid):
+            cfg = GpuConfig(80 + i, tokens // L, H, L, L, d, dt, causal, True)
+            peak = PEAK_BF16_TFLOPS if dt == "bf16" else PEAK_FP32_MFMA_TFLOPS
+            fwd_flop = config_flops(cfg) / 3  # 4 of the 12 B*H*L^2*d units
+            ms = run_config(T, cfg, args.steps, args.warmup)
+            fms = run_config(T, cfg, args.steps, args.warmup, part="fwd")
+            tf, ftf = config_flops(cfg) / (ms * 1e-3) / 1e12, fwd_flop / (fms * 1e-3) / 1e12
+            cases.append({"workload": f"{'causal' if causal else 'full'} attention {dt} B={cfg.B} H={H} L={L} d={d}",
+                          "dtype": dt, "fwd_ms": fms, "fwd_tflops": ftf, "step_ms": ms, "step_tflops": tf,
+                          "peak": peak, "step_frac_of_peak": tf / peak})
+            print(f"shapes {cases[-1]['workload']}: fwd {fms:.4f} ms {ftf:.1f} TF, fwd+bwd {ms:.4f} ms {tf:.1f} TF",
+                  file=sys.stderr, flush=True)
+        print(json.dumps({"metric": "attn forward and fwd+bwd TFLOP/s by head size, mask and dtype",
                           "steps": args.steps, "warmup": args.warmup, "cases": cases}), flush=True)
         return 0
 
