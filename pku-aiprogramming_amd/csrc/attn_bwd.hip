@@ -24,7 +24,7 @@
 // bf16: the dq kernel (attn_bwd_dq_pipe_kernel) runs first and also writes
 // the rows -D and LSE log2(e) the dkdv kernel reads; at d = 128 the dK / dV
 // role runs one wave per SIMD with 64 keys per wave (attn_bwd_w64.hip), at
-// d = 32 and 64 the kernel below.  fp32 (attn_bwd_f32.h): a separate row
+// d = 32 and 64, and for short causal heads at d = 128, the kernel below.  fp32 (attn_bwd_f32.h): a separate row
 // pre-pass (attn_bwd_delta_kernel), then one launch holding both roles.
 // All bf16 tiles are filled by direct global->LDS loads.  Loads past the end
 // of a sequence read a clamped (valid) row and the result is masked, so the
@@ -46,8 +46,17 @@ namespace tt {
 // than one 8-wave workgroup with a 4-deep ring.
 constexpr int bwd_nw(int) { return 4; }
 constexpr int kBwdStages = 2;
-// Query rows per LDS tile of the d <= 64 dK/dV kernel.
-constexpr int kDkdvBQ = 64;
+// Query rows per LDS tile of the two-waves-per-SIMD dK/dV kernel: 64, or 32
+// at d = 128, where two workgroups then fit the LDS of a CU (66.5 KB each).
+template <int D>
+constexpr int dkdv_bq() { return D >= 128 ? 32 : 64; }
+// The d = 128 dK/dV role: the one-wave-per-SIMD persistent kernel
+// (attn_bwd_w64.hip), except for causal heads of at most this many keys,
+// where each of its 256-key items is short and its prologue and epilogue
+// stand alone on the CU; the kernel below with two workgroups per CU then
+// overlaps them (dK/dV at L = 512 / 1024 / 2048: -30 / -17 / -8 %; at 4096,
+// and for non-causal heads, the one-wave kernel is 3-10 % faster).
+constexpr int64_t kDkdvTwoWaveMaxLk128 = 2048;
 
 // ND_i = -D_i = -sum_d dO[i][d] * O[i][d], one 16-byte chunk per thread
 // (stored negated: the dK/dV kernel starts its dP accumulator at -D, so the
@@ -91,7 +100,9 @@ __global__ __launch_bounds__(256) void attn_bwd_delta_kernel(const T* __restrict
 // ------------------------------------------------------------------ bf16 dK, dV
 // At d = 64 the compiler fits this kernel in 166-168 VGPRs, which lets three
 // workgroups share a CU (8 % faster than two); a change that needs more
-// registers silently drops it to two.  Stating the three-workgroup bound
+// registers silently drops it to two.  At d = 128 (short causal heads only,
+// kDkdvTwoWaveMaxLk128) it takes 251-252 VGPRs and 32-query tiles: two
+// workgroups per CU.  Stating the three-workgroup bound
 // instead produced other code and was 0-1 % slower; a variant with a second,
 // branch-free copy of the loop needed 248 VGPRs (152 spilled under the bound).
 template <int D, bool CAUSAL>
@@ -101,9 +112,8 @@ __global__ __launch_bounds__(64 * bwd_nw(D), 8 / bwd_nw(D)) void attn_bwd_dkdv_b
     u16* __restrict__ dK, u16* __restrict__ dV, int Lq, int Lk, int BH, int nkt, int order, float sl2,
     float scale) {
   using Tile = SwzTile<D>;
-  constexpr int NW = bwd_nw(D), BN = 32 * NW, BQ = kDkdvBQ, MT = BQ / 32, S = kBwdStages;
+  constexpr int NW = bwd_nw(D), BN = 32 * NW, BQ = dkdv_bq<D>(), MT = BQ / 32, S = kBwdStages;
   constexpr int NC = D / 16, ND = D / 32;
-  static_assert(D <= 64, "d = 128 runs the one-wave-per-SIMD kernel (attn_bwd_w64.hip)");
   constexpr int TE = Tile::kElems(BQ);
   constexpr int VS = 64;  // stride of the LSE / D row buffers (one 64-lane load each)
   using Dma = TileDma<D, BQ, NW>;
@@ -632,13 +642,11 @@ static int launch_bwd(const T* q, const T* k, const T* v, const T* o, const floa
     hipLaunchKernelGGL((attn_bwd_dq_pipe_kernel<D, CAUSAL>), dim3((unsigned)(nqp * BH)), dim3(256), 0, st, q, k, v, o,
                        dout, lse, l2, delta, dq, (int)Lq, (int)Lk, (int)BH, (int)nqp, gp, sl2, scale);
     TT_LAUNCHED("attention backward dQ launch", st);
-    if constexpr (D == 128) {
+    if (D == 128 && !(CAUSAL && Lk <= kDkdvTwoWaveMaxLk128))
       return launch_dkdv_w64(q, k, v, dout, l2, delta, dk, dv, BH, Lq, Lk, sl2, scale, CAUSAL, st);
-    } else {
-      hipLaunchKernelGGL((attn_bwd_dkdv_bf16_kernel<D, CAUSAL>), dim3((unsigned)(nkt * BH)), dim3(64 * NW), 0, st,
-                         q, k, v, dout, l2, delta, dk, dv, (int)Lq, (int)Lk, (int)BH, (int)nkt, gk, sl2, scale);
-      TT_LAUNCHED("attention backward dK/dV launch", st);
-    }
+    hipLaunchKernelGGL((attn_bwd_dkdv_bf16_kernel<D, CAUSAL>), dim3((unsigned)(nkt * BH)), dim3(64 * NW), 0, st, q,
+                       k, v, dout, l2, delta, dk, dv, (int)Lq, (int)Lk, (int)BH, (int)nkt, gk, sl2, scale);
+    TT_LAUNCHED("attention backward dK/dV launch", st);
   } else {
     constexpr int TPR = D / (16 / (int)sizeof(T));
     const int64_t dblk = (rows + (256 / TPR) - 1) / (256 / TPR);

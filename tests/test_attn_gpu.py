@@ -291,6 +291,34 @@ def test_persistent_dkdv_schedules_bf16(capi, B, H, L):
     _sampled_heads("sched", x, o, lse, dq, dk, dv, scale, True, [(bb, hh)], TOL["bf16"])
 
 
+# (B, H, L) of causal d = 128 launches on either side of the dK/dV kernel
+# choice: up to 2048 keys the two-waves-per-SIMD kernel (32-query tiles at
+# d = 128), beyond it the one-wave-per-SIMD persistent kernel.
+D128_CAUSAL_DKDV_PATHS = [
+    (2, 16, 2048),  # two-wave kernel, at the boundary
+    (4, 8, 1000),   # two-wave kernel, a ragged last key and query tile
+    (1, 8, 2056),   # one-wave kernel, just past the boundary (ragged)
+]
+
+
+@pytest.mark.parametrize("B,H,L", D128_CAUSAL_DKDV_PATHS)
+def test_d128_causal_dkdv_paths_bf16(capi, B, H, L):
+    """Both d = 128 dK/dV kernels near the length where the launcher switches
+    between them: every head against the fp32 kernels and through the
+    identities, two heads against the float64 oracle."""
+    d = 128
+    _say(f"d = 128 causal dK/dV path: bf16 B={B} H={H} L={L}")
+    rng = np.random.default_rng(7000 + L)
+    x = {n: orc.bf16_round(rng.standard_normal((B, H, L, d), dtype=np.float32)) for n in ("q", "k", "v", "do")}
+    scale = float(np.float32(1.0 / math.sqrt(d)))
+    b = _run_fwd(capi, x, "bf16", scale, True)
+    o, lse = b["o"].download(), b["lse"].download()
+    dq, dk, dv = _run_bwd(capi, b, x["do"], "bf16", scale, True)
+    _identities("d128", x, o, lse, dq, dk, dv, scale, True, TOL["bf16"])
+    _all_heads_vs_f32(capi, "d128", x, o, lse, dq, dk, dv, scale, True, TOL["bf16"])
+    _sampled_heads("d128", x, o, lse, dq, dk, dv, scale, True, [(0, 0), (B - 1, H - 1)], TOL["bf16"])
+
+
 DECODE_LONG_SPLITS = [
     # (B, H, Lkv, d): 512 heads -> five 2048-key splits per head, the last one
     # partial (808 keys), merged by the combine kernel
