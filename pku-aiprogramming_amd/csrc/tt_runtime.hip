@@ -13,6 +13,7 @@
 #include <map>
 #include <mutex>
 #include <string>
+#include <type_traits>
 #include <unordered_map>
 #include <vector>
 
@@ -163,72 +164,181 @@ __device__ __forceinline__ uint16_t f2bf(float f) {
 template <typename T> struct Num {
   __device__ static float ld(const T* p, int64_t i) { return (float)p[i]; }
   __device__ static void st(T* p, int64_t i, double v) { p[i] = (T)v; }
+  __device__ static float from(T x) { return (float)x; }
+  __device__ static T to(double v) { return (T)v; }
 };
 template <> struct Num<uint16_t> {  // bf16 storage
   __device__ static float ld(const uint16_t* p, int64_t i) { return bf2f(p[i]); }
   __device__ static void st(uint16_t* p, int64_t i, double v) { p[i] = f2bf((float)v); }
+  __device__ static float from(uint16_t x) { return bf2f(x); }
+  __device__ static uint16_t to(double v) { return f2bf((float)v); }
 };
 template <> struct Num<double> {
   __device__ static double ld(const double* p, int64_t i) { return p[i]; }
   __device__ static void st(double* p, int64_t i, double v) { p[i] = v; }
+  __device__ static double from(double x) { return x; }
+  __device__ static double to(double v) { return v; }
 };
 
-template <typename T>
-__global__ void k_elementwise(int op, T* c, const T* a, const T* b, int64_t n, double alpha,
-                              double beta, uint64_t seed) {
-  int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
-    double r = 0.0;
-    switch (op) {
-      case TT_EW_ADD: r = (double)Num<T>::ld(a, i) + (double)Num<T>::ld(b, i); break;
-      case TT_EW_SUB: r = (double)Num<T>::ld(a, i) - (double)Num<T>::ld(b, i); break;
-      case TT_EW_FILL: r = alpha; break;
-      case TT_EW_NEG: r = -(double)Num<T>::ld(a, i); break;
-      case TT_EW_SCALE: r = (double)Num<T>::ld(a, i) * alpha; break;
-      case TT_EW_RELU: { double x = Num<T>::ld(a, i); r = x > 0 ? x : 0; } break;
-      case TT_EW_RELU_BWD: r = Num<T>::ld(a, i) > 0 ? (double)Num<T>::ld(b, i) : 0.0; break;
-      case TT_EW_SIGMOID: r = 1.0 / (1.0 + exp(-(double)Num<T>::ld(a, i))); break;
-      case TT_EW_SIGMOID_BWD: {
-        double s = 1.0 / (1.0 + exp(-(double)Num<T>::ld(a, i)));
-        r = s * (1.0 - s) * (double)Num<T>::ld(b, i);
-      } break;
-      case TT_EW_UNIFORM: {
-        double u = u01(splitmix64(seed ^ splitmix64((uint64_t)i)));
-        r = alpha + (beta - alpha) * u;
-      } break;
-    }
-    Num<T>::st(c, i, r);
+// One element of tt_elementwise: element i of c from the stored values x = a[i]
+// and y = b[i] (zero where the op reads no such operand).  Floating storage
+// computes in double and rounds once on the store (for add, sub and scale of
+// floats this is the correctly rounded float result); int32 keeps integer
+// arithmetic where the reference has it (add / sub / neg / scale).
+template <int OP, typename T>
+__device__ __forceinline__ T ew_one(T xs, T ys, int64_t i, double alpha, double beta, uint64_t seed) {
+  const double x = Num<T>::from(xs), y = Num<T>::from(ys);
+  double r = 0.0;
+  if constexpr (OP == TT_EW_ADD) r = x + y;
+  else if constexpr (OP == TT_EW_SUB) r = x - y;
+  else if constexpr (OP == TT_EW_FILL) r = alpha;
+  else if constexpr (OP == TT_EW_NEG) r = -x;
+  else if constexpr (OP == TT_EW_SCALE) r = x * alpha;
+  else if constexpr (OP == TT_EW_RELU) r = x > 0 ? x : 0;
+  else if constexpr (OP == TT_EW_RELU_BWD) r = x > 0 ? y : 0.0;
+  else if constexpr (OP == TT_EW_SIGMOID) r = 1.0 / (1.0 + exp(-x));
+  else if constexpr (OP == TT_EW_SIGMOID_BWD) {
+    const double s = 1.0 / (1.0 + exp(-x));
+    r = s * (1.0 - s) * y;
+  } else if constexpr (OP == TT_EW_UNIFORM) {
+    r = alpha + (beta - alpha) * u01(splitmix64(seed ^ splitmix64((uint64_t)i)));
+  }
+  return Num<T>::to(r);
+}
+template <int OP>
+__device__ __forceinline__ int32_t ew_one_i32(int32_t x, int32_t y, int64_t i, double alpha, double beta,
+                                              uint64_t seed) {
+  if constexpr (OP == TT_EW_ADD) return x + y;
+  else if constexpr (OP == TT_EW_SUB) return x - y;
+  else if constexpr (OP == TT_EW_FILL) return (int32_t)alpha;
+  else if constexpr (OP == TT_EW_NEG) return -x;
+  else if constexpr (OP == TT_EW_SCALE) return (int32_t)(x * (int32_t)alpha);
+  else if constexpr (OP == TT_EW_RELU) return x > 0 ? x : 0;
+  else if constexpr (OP == TT_EW_RELU_BWD) return x > 0 ? y : 0;
+  else if constexpr (OP == TT_EW_SIGMOID) return (int32_t)(1.0 / (1.0 + exp(-(double)x)));
+  else if constexpr (OP == TT_EW_SIGMOID_BWD) {
+    const double s = 1.0 / (1.0 + exp(-(double)x));
+    return (int32_t)(s * (1.0 - s) * y);
+  } else {
+    // inclusive integer range [alpha, beta] like std::uniform_int_distribution
+    const int64_t lo = (int64_t)alpha, hi = (int64_t)beta;
+    const uint64_t span = (uint64_t)(hi - lo + 1);
+    return (int32_t)(lo + (int64_t)(splitmix64(seed ^ splitmix64((uint64_t)i)) % span));
   }
 }
-// Integer storage: do integer arithmetic where it matters (add/sub/neg/scale).
-template <>
-__global__ void k_elementwise<int32_t>(int op, int32_t* c, const int32_t* a, const int32_t* b,
-                                       int64_t n, double alpha, double beta, uint64_t seed) {
-  int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
-    int32_t r = 0;
-    switch (op) {
-      case TT_EW_ADD: r = a[i] + b[i]; break;
-      case TT_EW_SUB: r = a[i] - b[i]; break;
-      case TT_EW_FILL: r = (int32_t)alpha; break;
-      case TT_EW_NEG: r = -a[i]; break;
-      case TT_EW_SCALE: r = (int32_t)(a[i] * (int32_t)alpha); break;
-      case TT_EW_RELU: r = a[i] > 0 ? a[i] : 0; break;
-      case TT_EW_RELU_BWD: r = a[i] > 0 ? b[i] : 0; break;
-      case TT_EW_SIGMOID: r = (int32_t)(1.0 / (1.0 + exp(-(double)a[i]))); break;
-      case TT_EW_SIGMOID_BWD: {
-        double s = 1.0 / (1.0 + exp(-(double)a[i]));
-        r = (int32_t)(s * (1.0 - s) * b[i]);
-      } break;
-      case TT_EW_UNIFORM: {
-        // Inclusive integer range [alpha, beta] like std::uniform_int_distribution.
-        int64_t lo = (int64_t)alpha, hi = (int64_t)beta;
-        uint64_t span = (uint64_t)(hi - lo + 1);
-        r = (int32_t)(lo + (int64_t)(splitmix64(seed ^ splitmix64((uint64_t)i)) % span));
-      } break;
-    }
-    c[i] = r;
+template <int OP, typename T>
+__device__ __forceinline__ T ew_elem(T x, T y, int64_t i, double alpha, double beta, uint64_t seed) {
+  if constexpr (std::is_same<T, int32_t>::value)
+    return ew_one_i32<OP>(x, y, i, alpha, beta, seed);
+  else
+    return ew_one<OP, T>(x, y, i, alpha, beta, seed);
+}
+
+constexpr bool ew_reads_a(int op) { return !(op == TT_EW_FILL || op == TT_EW_UNIFORM); }
+constexpr bool ew_reads_b(int op) {
+  return op == TT_EW_ADD || op == TT_EW_SUB || op == TT_EW_RELU_BWD || op == TT_EW_SIGMOID_BWD;
+}
+
+// Any alignment: one element per thread and step of a grid-stride loop.
+template <int OP, typename T>
+__device__ void ew_scalar_loop(T* c, const T* a, const T* b, int64_t n, double alpha, double beta,
+                               uint64_t seed) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+    c[i] = ew_elem<OP, T>(ew_reads_a(OP) ? a[i] : T(0), ew_reads_b(OP) ? b[i] : T(0), i, alpha, beta, seed);
+}
+
+// 16-byte aligned operands: 16 bytes of each operand per thread, a grid of
+// one thread per 16-byte word up to 2^24 workgroups (a grid-stride loop
+// beyond), and the n % V tail elements done one by one by the first threads.
+// One word per thread over the full grid measured fastest for a 1 GiB f32
+// scale (6.5 TB/s, against 5.3-5.7 with four words per thread or the grid
+// capped at 65536 workgroups).  NT: non-temporal loads and stores, for
+// operands too large to stay in the 256 MB Infinity Cache (1 GiB: 6.5 against
+// 6.2 TB/s); smaller ones keep ordinary accesses (64 MiB, repeated: 6.8
+// against 6.0 TB/s).
+typedef unsigned int ew_u32x4 __attribute__((ext_vector_type(4)));
+constexpr int64_t kEwMaxBlocks = int64_t(1) << 24;
+constexpr int64_t kEwNtBytes = int64_t(256) << 20;
+template <bool NT>
+__device__ __forceinline__ ew_u32x4 ew_ld16(const void* p, int64_t v) {
+  const ew_u32x4* q = reinterpret_cast<const ew_u32x4*>(p) + v;
+  if constexpr (NT) return __builtin_nontemporal_load(q);
+  return *q;
+}
+template <bool NT>
+__device__ __forceinline__ void ew_st16(void* p, int64_t v, ew_u32x4 x) {
+  ew_u32x4* q = reinterpret_cast<ew_u32x4*>(p) + v;
+  if constexpr (NT)
+    __builtin_nontemporal_store(x, q);
+  else
+    *q = x;
+}
+template <int OP, typename T, bool NT>
+__device__ void ew_vec_loop(T* c, const T* a, const T* b, int64_t n, double alpha, double beta, uint64_t seed) {
+  constexpr int V = 16 / sizeof(T);
+  union Pack {
+    ew_u32x4 u;
+    T e[V];
+  };
+  const int64_t nv = n / V;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  const int64_t t0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  for (int64_t v = t0; v < nv; v += stride) {
+    Pack pa, pb, pc;
+    pa.u = ew_u32x4{0, 0, 0, 0};
+    pb.u = ew_u32x4{0, 0, 0, 0};
+    if constexpr (ew_reads_a(OP)) pa.u = ew_ld16<NT>(a, v);
+    if constexpr (ew_reads_b(OP)) pb.u = ew_ld16<NT>(b, v);
+#pragma unroll
+    for (int e = 0; e < V; ++e) pc.e[e] = ew_elem<OP, T>(pa.e[e], pb.e[e], v * V + e, alpha, beta, seed);
+    ew_st16<NT>(c, v, pc.u);
   }
+  const int64_t i = nv * V + t0;
+  if (i < n)
+    c[i] = ew_elem<OP, T>(ew_reads_a(OP) ? a[i] : T(0), ew_reads_b(OP) ? b[i] : T(0), i, alpha, beta, seed);
+}
+
+// MODE 0: one element per thread (any alignment); 1: 16-byte words; 2: 16-byte
+// words, non-temporal.
+template <int MODE, int OP, typename T>
+__device__ __forceinline__ void ew_run(T* c, const T* a, const T* b, int64_t n, double alpha, double beta,
+                                       uint64_t seed) {
+  if constexpr (MODE == 0)
+    ew_scalar_loop<OP, T>(c, a, b, n, alpha, beta, seed);
+  else
+    ew_vec_loop<OP, T, MODE == 2>(c, a, b, n, alpha, beta, seed);
+}
+
+// The op is uniform over the launch: one switch outside the loop, each case a
+// loop specialised for its op.
+template <int MODE, typename T>
+__device__ void ew_dispatch(int op, T* c, const T* a, const T* b, int64_t n, double alpha, double beta,
+                            uint64_t seed) {
+  switch (op) {
+    case TT_EW_ADD: ew_run<MODE, TT_EW_ADD, T>(c, a, b, n, alpha, beta, seed); break;
+    case TT_EW_SUB: ew_run<MODE, TT_EW_SUB, T>(c, a, b, n, alpha, beta, seed); break;
+    case TT_EW_FILL: ew_run<MODE, TT_EW_FILL, T>(c, a, b, n, alpha, beta, seed); break;
+    case TT_EW_NEG: ew_run<MODE, TT_EW_NEG, T>(c, a, b, n, alpha, beta, seed); break;
+    case TT_EW_SCALE: ew_run<MODE, TT_EW_SCALE, T>(c, a, b, n, alpha, beta, seed); break;
+    case TT_EW_RELU: ew_run<MODE, TT_EW_RELU, T>(c, a, b, n, alpha, beta, seed); break;
+    case TT_EW_RELU_BWD: ew_run<MODE, TT_EW_RELU_BWD, T>(c, a, b, n, alpha, beta, seed); break;
+    case TT_EW_SIGMOID: ew_run<MODE, TT_EW_SIGMOID, T>(c, a, b, n, alpha, beta, seed); break;
+    case TT_EW_SIGMOID_BWD: ew_run<MODE, TT_EW_SIGMOID_BWD, T>(c, a, b, n, alpha, beta, seed); break;
+    case TT_EW_UNIFORM: ew_run<MODE, TT_EW_UNIFORM, T>(c, a, b, n, alpha, beta, seed); break;
+    default: break;
+  }
+}
+
+template <typename T, bool NT>
+__global__ __launch_bounds__(256) void k_elementwise(int op, T* c, const T* a, const T* b, int64_t n,
+                                                     double alpha, double beta, uint64_t seed) {
+  ew_dispatch<NT ? 2 : 1, T>(op, c, a, b, n, alpha, beta, seed);
+}
+template <typename T>
+__global__ __launch_bounds__(256) void k_elementwise_scalar(int op, T* c, const T* a, const T* b, int64_t n,
+                                                            double alpha, double beta, uint64_t seed) {
+  ew_dispatch<0, T>(op, c, a, b, n, alpha, beta, seed);
 }
 
 // scale * N(0,1) by Box-Muller on two 24-bit uniforms of splitmix64(seed, i).
@@ -480,24 +590,31 @@ int tt_elementwise(int op, int dtype, void* c, const void* a, const void* b, int
   int rc = ensure_init();
   if (rc) return rc;
   hipStream_t s = stream_or_default(stream);
-  int g = grid_for(n);
+  auto aligned = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+  const bool vec = aligned(c) && (!need_a || aligned(a)) && (!need_b || aligned(b));
+  auto launch = [&](auto tag) {
+    using T = decltype(tag);
+    if (vec) {
+      const int64_t nv = n / (int64_t)(16 / sizeof(T));
+      int64_t g = (nv + 255) / 256;
+      g = g < 1 ? 1 : (g > kEwMaxBlocks ? kEwMaxBlocks : g);
+      const int64_t bytes = n * (int64_t)sizeof(T) * (1 + (need_a ? 1 : 0) + (need_b ? 1 : 0));
+      if (bytes >= kEwNtBytes)
+        hipLaunchKernelGGL((k_elementwise<T, true>), dim3((unsigned)g), dim3(256), 0, s, op, (T*)c,
+                           (const T*)a, (const T*)b, n, alpha, beta, seed);
+      else
+        hipLaunchKernelGGL((k_elementwise<T, false>), dim3((unsigned)g), dim3(256), 0, s, op, (T*)c,
+                           (const T*)a, (const T*)b, n, alpha, beta, seed);
+    } else {
+      hipLaunchKernelGGL(k_elementwise_scalar<T>, dim3(grid_for(n)), dim3(256), 0, s, op, (T*)c, (const T*)a,
+                         (const T*)b, n, alpha, beta, seed);
+    }
+  };
   switch (dtype) {
-    case TT_F32:
-      hipLaunchKernelGGL(k_elementwise<float>, dim3(g), dim3(256), 0, s, op, (float*)c,
-                         (const float*)a, (const float*)b, n, alpha, beta, seed);
-      break;
-    case TT_F64:
-      hipLaunchKernelGGL(k_elementwise<double>, dim3(g), dim3(256), 0, s, op, (double*)c,
-                         (const double*)a, (const double*)b, n, alpha, beta, seed);
-      break;
-    case TT_I32:
-      hipLaunchKernelGGL(k_elementwise<int32_t>, dim3(g), dim3(256), 0, s, op, (int32_t*)c,
-                         (const int32_t*)a, (const int32_t*)b, n, alpha, beta, seed);
-      break;
-    case TT_BF16:
-      hipLaunchKernelGGL(k_elementwise<uint16_t>, dim3(g), dim3(256), 0, s, op, (uint16_t*)c,
-                         (const uint16_t*)a, (const uint16_t*)b, n, alpha, beta, seed);
-      break;
+    case TT_F32: launch(float{}); break;
+    case TT_F64: launch(double{}); break;
+    case TT_I32: launch(int32_t{}); break;
+    case TT_BF16: launch(uint16_t{}); break;
     default:
       return fail(TT_ERR_ARG, "tt_elementwise: bad dtype");
   }

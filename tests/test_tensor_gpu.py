@@ -145,3 +145,57 @@ def test_bf16_repr_and_shape_errors(mt):
     assert "Shape: [3]" in repr(t)
     with pytest.raises(ValueError, match="Shape mismatch"):
         t + mt.Tensor_bf16(np.zeros(4, np.float32), "gpu")
+
+
+EW_OPS = {"add": 0, "sub": 1, "fill": 2, "neg": 3, "scale": 4, "relu": 5, "relu_bwd": 6, "sigmoid": 7,
+          "sigmoid_bwd": 8, "uniform": 9}
+CAPI_DT = {"float": ("f32", 0, np.float32), "double": ("f64", 1, np.float64), "int": ("i32", 2, np.int32),
+           "bf16": ("bf16", 3, np.uint16)}
+
+
+@pytest.mark.parametrize("dt", DTYPES)
+@pytest.mark.parametrize("n", [1, 7, 13, 4099, 100_003])
+def test_elementwise_vector_and_scalar_paths_agree(dt, n):
+    """tt_elementwise takes a 16-byte vector kernel when every operand is
+    16-byte aligned (the n % (16 / itemsize) tail elements done one by one)
+    and a one-element-per-thread kernel otherwise.  Run every op on aligned
+    buffers and on the same values one element past the start of a block
+    (misaligned for every dtype); the stored bytes must be identical, and the
+    aligned result equals numpy's where the op is exact."""
+    import tt_capi as capi
+
+    name, code, raw = CAPI_DT[dt]
+    item = capi.DeviceBuffer.ITEM[name]
+    x, y = _vals(dt, n, 11).ravel(), _vals(dt, n, 12).ravel()
+    L = capi.lib()
+
+    def buffers(off):
+        bufs = []
+        for v in (x, y, None):
+            b = capi.DeviceBuffer((n + 1,), name)
+            if v is not None:
+                host = np.concatenate([np.zeros(1, v.dtype), v]) if off else np.concatenate([v, np.zeros(1, v.dtype)])
+                b.upload(host)
+            bufs.append(b)
+        return bufs
+
+    alpha, beta = (3.0, 9.0) if dt == "int" else (0.75, 2.5)
+    for op, k in EW_OPS.items():
+        out = []
+        for off in (0, 1):
+            ba, bb, bc = buffers(off)
+            sh = off * item
+            L.call("tt_elementwise", k, code, bc.ptr + sh, ba.ptr + sh, bb.ptr + sh, n, alpha, beta, 5, None)
+            L.sync()
+            got = bc.download_bytes().view(raw)
+            out.append(got[off:off + n].copy())
+        np.testing.assert_array_equal(out[0], out[1], err_msg=f"{dt} {op} n={n}")
+        if op in ("add", "sub", "neg") or (op == "scale" and dt != "int"):
+            wide = np.float64 if dt != "int" else np.int64
+            ref = {"add": x.astype(wide) + y, "sub": x.astype(wide) - y, "neg": -x.astype(wide),
+                   "scale": x.astype(np.float64) * alpha}[op]
+            want = _round(dt, ref)
+            if dt == "bf16":
+                want = want.astype(np.float32).view(np.uint32) >> 16
+            np.testing.assert_array_equal(out[0].astype(np.int64), np.asarray(want).astype(np.int64),
+                                          err_msg=f"{dt} {op} n={n}")
