@@ -138,6 +138,52 @@ def run_fwdbwd(T, steps, warmup):
     return total_ms / steps, per
 
 
+def run_pcie(T, reps=3):
+    """The c5 step as a reference user runs it, host to host: fp32 numpy Q, K, V
+    and dO (the reference's TinyTensor-from-numpy inputs) uploaded to bf16 device
+    buffers (converted in the staging pass), forward + backward, and O, dQ, dK,
+    dV downloaded to fp32 numpy.  Reported beside the bench line, never as its
+    value (which times the step on HBM-resident inputs)."""
+    import numpy as np
+
+    B, H, L, d = C5["B"], C5["H"], C5["L"], C5["d"]
+    scale = float(np.float32(1.0 / math.sqrt(d)))
+    shp = (B, H, L, d)
+    n = B * H * L * d
+    rng = np.random.default_rng(5)
+    host_in = [rng.standard_normal(shp, dtype=np.float32) for _ in range(4)]
+    host_out = [np.empty(shp, np.float32) for _ in range(4)]
+    q, k, v, do = (T.DeviceBuffer(shp, "bf16") for _ in range(4))
+    o, dq, dk, dv = (T.DeviceBuffer(shp, "bf16") for _ in range(4))
+    lse = T.DeviceBuffer((B, H, L), "f32")
+    Lb = T.lib()
+
+    def once():
+        t0 = time.perf_counter()
+        for h, b in zip(host_in, (q, k, v, do)):
+            Lb.call("tt_upload_bf16_from_f32", b.ptr, h.ctypes.data, n)
+        Lb.sync()
+        t1 = time.perf_counter()
+        T.attn_fwd(q, k, v, o, lse, scale, True)
+        T.attn_bwd(q, k, v, o, lse, do, dq, dk, dv, scale, True)
+        Lb.sync()
+        t2 = time.perf_counter()
+        for h, b in zip(host_out, (o, dq, dk, dv)):
+            Lb.call("tt_download_bf16_to_f32", h.ctypes.data, b.ptr, n)
+        Lb.sync()
+        t3 = time.perf_counter()
+        return t3 - t0, t1 - t0, t2 - t1, t3 - t2
+
+    once()
+    best = min((once() for _ in range(reps)), key=lambda r: r[0])
+    flops = fwdbwd_flops(**C5)
+    return {"metric": "c5 fwd+bwd host to host (fp32 numpy in and out, bf16 on the device)",
+            "ms_per_step": best[0] * 1e3, "value": flops / best[0] / 1e12, "unit": "TFLOP/s",
+            "upload_ms": best[1] * 1e3, "compute_ms": best[2] * 1e3, "download_ms": best[3] * 1e3,
+            "host_bytes_per_step": 8 * n * 4, "reps": reps,
+            "config": {"workload": "causal attention fwd+bwd, B=4 H=32 L=4096 d=128, fp32 host arrays"}}
+
+
 def run_decode(T, steps, warmup):
     B, H, Lkv, d = C4["B"], C4["H"], C4["Lkv"], C4["d"]
     scale = float(__import__("numpy").float32(1.0 / math.sqrt(d)))
@@ -630,12 +676,12 @@ def main(argv=None):
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--only", choices=["all", "fwdbwd", "configs", "decode", "copy", "ceiling", "softmax", "gemm", "io",
-                                       "sustain", "seqsweep", "shapes"],
+                                       "sustain", "seqsweep", "shapes", "pcie"],
                     default="all",
                     help="run one workload only (for profiler runs; 'copy' is the 1 GiB calibration copy, "
                          "'ceiling' the library bf16 GEMM reference, 'sustain' the --sustain loop, 'seqsweep' "
                          "the c5 step at L = 1024 .. 16384 over the same number of tokens, 'shapes' every head "
-                         "size, causal and not, in both dtypes)")
+                         "size, causal and not, in both dtypes, 'pcie' the c5 step host to host)")
     ap.add_argument("--sustain", default="3:all:8", metavar="CID:PART:SECONDS",
                     help="with --only sustain: config (1, 2, 3 or 5), part (all, fwd or bwd) and duration of a "
                          "loop of 200-step batches")
@@ -719,6 +765,10 @@ def main(argv=None):
                    "B": C5["B"], "H": C5["H"], "L": C5["L"], "d": C5["d"], "causal": True,
                    "flop_per_step": fwdbwd_flops(**C5)},
     }
+
+    if args.only == "pcie":
+        print(json.dumps(run_pcie(T)), flush=True)
+        return 0
 
     if args.only == "copy":
         ms, gbs = run_copy(T, args.steps, args.warmup)
