@@ -7,6 +7,9 @@ scales from 0.25 to 4, so that the softmax ranges from nearly uniform to
 nearly one-hot (score spreads far past the forward's lazy-rescale threshold
 of 8 in the log2 domain, which moves the running max mid-row).
 
+Six bf16 d = 128 cases lie around 2048 keys, where causal heads switch between
+the two dK/dV kernels.
+
 A few structured inputs pin behaviour a random draw rarely reaches:
 identical keys (uniform weights: O = mean of V, LSE = ln(#keys) + s q.k),
 dO = 0 (all gradients exactly 0), and one key far larger than the rest.
@@ -62,6 +65,23 @@ CASES = _cases()
 # head counts that are multiples of 8: the launches' per-XCD head groups and,
 # for causal d <= 64, the held-back cheap tiles (attn_tiles.h)
 CASES += _cases(16, seed=2025, heads=[(1, 8), (2, 8), (1, 16), (3, 8)], lmax=1500, base=6000)
+
+
+def _switch_cases(n=6, seed=2026, base=7000):
+    """bf16 d = 128 around 2048 keys, where causal heads move from the
+    two-waves-per-SIMD dK/dV kernel (Lk <= 2048) to the persistent one."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        causal = i < 4
+        Lq = int(rng.integers(1990, 2110))
+        Lk = Lq if causal else int(rng.integers(1990, 2110))
+        B, H = [(1, 2), (1, 3), (2, 1)][int(rng.integers(0, 3))]
+        out.append((B, H, Lq, Lk, 128, causal, float(rng.choice([0.5, 1.0, 2.0])), "bf16", base + i))
+    return out
+
+
+CASES += _switch_cases()
 
 
 def _inputs(B, H, Lq, Lk, d, sigma, dtype, seed):
