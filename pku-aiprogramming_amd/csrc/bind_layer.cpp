@@ -1,4 +1,4 @@
-// Module `myLayer`: the attention entry points and SoftmaxForward, bound in the style of
+// Module `myLayer`: the attention entry points, SoftmaxForward and FcForward / FcBackward, bound in the style of
 // Task3/Tinytensor/src/bind_Layer.cpp:10-24 (free functions over TinyTensor
 // references), with float and bf16 overloads.
 #include <pybind11/pybind11.h>
@@ -29,4 +29,11 @@ PYBIND11_MODULE(myLayer, m) {
         py::arg("out"), py::arg("scale"));
   // the reference binds SoftmaxForward<float> positionally (bind_Layer.cpp:20)
   m.def("SoftmaxForward", &SoftmaxForward<float>, py::arg("input"), py::arg("output"));
+  // positional as in the reference (bind_Layer.cpp:12-13), plus bf16 overloads
+  m.def("FcForward", &FcForward<float>, py::arg("input"), py::arg("output"), py::arg("weight"), py::arg("bias"));
+  m.def("FcForward", &FcForward<bf16>, py::arg("input"), py::arg("output"), py::arg("weight"), py::arg("bias"));
+  m.def("FcBackward", &FcBackward<float>, py::arg("input"), py::arg("output"), py::arg("weight"), py::arg("bias"),
+        py::arg("grad_input"), py::arg("grad_output"), py::arg("grad_weight"), py::arg("grad_bias"));
+  m.def("FcBackward", &FcBackward<bf16>, py::arg("input"), py::arg("output"), py::arg("weight"), py::arg("bias"),
+        py::arg("grad_input"), py::arg("grad_output"), py::arg("grad_weight"), py::arg("grad_bias"));
 }

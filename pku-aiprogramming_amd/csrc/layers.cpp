@@ -1,4 +1,4 @@
-// Attention and softmax layer functions: shape checks, output sizing, then one C-ABI call.
+// Attention, softmax and fully connected layer functions: shape checks, output sizing, then the C-ABI calls.
 #include "layers.h"
 
 #include <initializer_list>
@@ -163,6 +163,132 @@ void SoftmaxForward(const TinyTensor<T>& input, TinyTensor<T>& output) {
   tt_check(tt_sync(), fn.c_str());
 }
 
+namespace {
+
+// C = alpha op(A) op(B) + beta C on the library GEMM (row-major, tt_gemm_*).
+template <typename T>
+void gemm(const char* fn, bool ta, bool tb, int64_t m, int64_t n, int64_t k, float alpha, const T* A, const T* B,
+          float beta, T* C) {
+  int rc;
+  if constexpr (std::is_same<T, float>::value)
+    rc = tt_gemm_f32(ta ? 1 : 0, tb ? 1 : 0, m, n, k, alpha, A, B, beta, C, nullptr);
+  else
+    rc = tt_gemm_bf16(ta ? 1 : 0, tb ? 1 : 0, m, n, k, alpha, reinterpret_cast<const uint16_t*>(A),
+                      reinterpret_cast<const uint16_t*>(B), beta, reinterpret_cast<uint16_t*>(C), nullptr);
+  tt_check(rc, fn);
+}
+
+struct FcDims {
+  int64_t batch, fin, fout;
+  bool scalar_bias;
+};
+
+// The reference's reading of the shapes (Layers.cu:16-24, 28): every axis of
+// input but the last is a batch axis, weight is [fin, fout], a bias of shape
+// [1] is one value for every output, any other bias is the [fout] row.
+template <typename T>
+FcDims fc_dims(const std::string& fn, const TinyTensor<T>& input, const TinyTensor<T>& weight,
+               const TinyTensor<T>& bias) {
+  need_gpu(fn, "input", input.device);
+  need_gpu(fn, "weight", weight.device);
+  need_gpu(fn, "bias", bias.device);
+  if (input.shape.empty()) throw std::invalid_argument(fn + ": input must have rank >= 1");
+  if (weight.shape.size() != 2) throw std::invalid_argument(fn + ": weight must have rank 2 [fin, fout]");
+  FcDims f;
+  f.batch = 1;
+  for (size_t i = 0; i + 1 < input.shape.size(); ++i) f.batch *= input.shape[i];
+  f.fin = input.shape.back();
+  f.fout = weight.shape[1];
+  if (weight.shape[0] != f.fin)
+    throw std::invalid_argument(fn + ": weight rows (" + std::to_string(weight.shape[0]) +
+                                ") must equal the input's last axis (" + std::to_string(f.fin) + ")");
+  f.scalar_bias = bias.shape.size() == 1 && bias.shape[0] == 1;
+  if (!f.scalar_bias && (int64_t)bias.size != f.fout)
+    throw std::invalid_argument(fn + ": bias must hold fout (" + std::to_string(f.fout) + ") values or be [1]");
+  return f;
+}
+
+}  // namespace
+
+template <typename T>
+void FcForward(const TinyTensor<T>& input, TinyTensor<T>& output, const TinyTensor<T>& weight,
+               const TinyTensor<T>& bias) {
+  const std::string fn = "FcForward";
+  const FcDims f = fc_dims(fn, input, weight, bias);
+  need_gpu(fn, "output", output.device);
+  no_alias(fn, {{input.p_data, "input"}, {weight.p_data, "weight"}, {bias.p_data, "bias"}},
+           {{output.p_data, "output"}});
+  std::vector<int> oshape(input.shape.begin(), input.shape.end() - 1);
+  oshape.push_back((int)f.fout);
+  output.resize(oshape);
+  if (f.batch == 0 || f.fout == 0) return;
+  gemm<T>(fn.c_str(), false, false, f.batch, f.fout, f.fin, 1.f, input.p_data, weight.p_data, 0.f, output.p_data);
+  TinyTensor<T> ones(std::vector<int>{(int)f.batch, 1}, "gpu");
+  ones.ones();
+  if (f.scalar_bias) {
+    TinyTensor<T> row(std::vector<int>{1, (int)f.fout}, "gpu");
+    row.floatks((float)bias.get_data()[0]);
+    gemm<T>(fn.c_str(), false, false, f.batch, f.fout, 1, 1.f, ones.p_data, row.p_data, 1.f, output.p_data);
+    tt_check(tt_sync(), fn.c_str());
+  } else {
+    gemm<T>(fn.c_str(), false, false, f.batch, f.fout, 1, 1.f, ones.p_data, bias.p_data, 1.f, output.p_data);
+    tt_check(tt_sync(), fn.c_str());
+  }
+}
+
+template <typename T>
+void FcBackward(const TinyTensor<T>& input, const TinyTensor<T>& output, const TinyTensor<T>& weight,
+                const TinyTensor<T>& bias, TinyTensor<T>& grad_input, const TinyTensor<T>& grad_output,
+                TinyTensor<T>& grad_weight, TinyTensor<T>& grad_bias) {
+  (void)output;
+  const std::string fn = "FcBackward";
+  const FcDims f = fc_dims(fn, input, weight, bias);
+  need_gpu(fn, "grad_output", grad_output.device);
+  need_gpu(fn, "grad_input", grad_input.device);
+  need_gpu(fn, "grad_weight", grad_weight.device);
+  need_gpu(fn, "grad_bias", grad_bias.device);
+  if ((int64_t)grad_output.size != f.batch * f.fout || grad_output.shape.empty() ||
+      grad_output.shape.back() != f.fout)
+    throw std::invalid_argument(fn + ": grad_output must be [.., fout] with the input's batch axes");
+  no_alias(fn,
+           {{input.p_data, "input"}, {weight.p_data, "weight"}, {bias.p_data, "bias"},
+            {grad_output.p_data, "grad_output"}},
+           {{grad_input.p_data, "grad_input"}, {grad_weight.p_data, "grad_weight"}, {grad_bias.p_data, "grad_bias"}});
+  grad_input.resize(input.shape);
+  grad_weight.resize(weight.shape);
+  grad_bias.resize(bias.shape);
+  if (f.batch == 0) {  // no rows: every gradient is a sum over nothing
+    grad_weight.zeros();
+    grad_bias.zeros();
+    tt_check(tt_sync(), fn.c_str());
+    return;
+  }
+  if (f.fout == 0) {
+    grad_input.zeros();
+    grad_bias.zeros();
+    tt_check(tt_sync(), fn.c_str());
+    return;
+  }
+  gemm<T>(fn.c_str(), false, true, f.batch, f.fin, f.fout, 1.f, grad_output.p_data, weight.p_data, 0.f,
+          grad_input.p_data);
+  gemm<T>(fn.c_str(), true, false, f.fin, f.fout, f.batch, 1.f, input.p_data, grad_output.p_data, 0.f,
+          grad_weight.p_data);
+  TinyTensor<T> ones(std::vector<int>{1, (int)f.batch}, "gpu");
+  ones.ones();
+  if (f.scalar_bias) {
+    TinyTensor<T> row(std::vector<int>{1, (int)f.fout}, "gpu");
+    gemm<T>(fn.c_str(), false, false, 1, f.fout, f.batch, 1.f, ones.p_data, grad_output.p_data, 0.f, row.p_data);
+    TinyTensor<T> col(std::vector<int>{(int)f.fout, 1}, "gpu");
+    col.ones();
+    gemm<T>(fn.c_str(), false, false, 1, 1, f.fout, 1.f, row.p_data, col.p_data, 0.f, grad_bias.p_data);
+    tt_check(tt_sync(), fn.c_str());
+  } else {
+    gemm<T>(fn.c_str(), false, false, 1, f.fout, f.batch, 1.f, ones.p_data, grad_output.p_data, 0.f,
+            grad_bias.p_data);
+    tt_check(tt_sync(), fn.c_str());
+  }
+}
+
 template void AttentionForward<float>(const TinyTensor<float>&, const TinyTensor<float>&, const TinyTensor<float>&,
                                       TinyTensor<float>&, TinyTensor<float>&, float, bool);
 template void AttentionForward<bf16>(const TinyTensor<bf16>&, const TinyTensor<bf16>&, const TinyTensor<bf16>&,
@@ -178,3 +304,13 @@ template void AttentionDecode<float>(const TinyTensor<float>&, const TinyTensor<
 template void AttentionDecode<bf16>(const TinyTensor<bf16>&, const TinyTensor<bf16>&, const TinyTensor<bf16>&,
                                     TinyTensor<bf16>&, float);
 template void SoftmaxForward<float>(const TinyTensor<float>&, TinyTensor<float>&);
+template void FcForward<float>(const TinyTensor<float>&, TinyTensor<float>&, const TinyTensor<float>&,
+                               const TinyTensor<float>&);
+template void FcForward<bf16>(const TinyTensor<bf16>&, TinyTensor<bf16>&, const TinyTensor<bf16>&,
+                              const TinyTensor<bf16>&);
+template void FcBackward<float>(const TinyTensor<float>&, const TinyTensor<float>&, const TinyTensor<float>&,
+                                const TinyTensor<float>&, TinyTensor<float>&, const TinyTensor<float>&,
+                                TinyTensor<float>&, TinyTensor<float>&);
+template void FcBackward<bf16>(const TinyTensor<bf16>&, const TinyTensor<bf16>&, const TinyTensor<bf16>&,
+                               const TinyTensor<bf16>&, TinyTensor<bf16>&, const TinyTensor<bf16>&,
+                               TinyTensor<bf16>&, TinyTensor<bf16>&);

@@ -1,4 +1,4 @@
-// Attention and softmax layer functions of the `myLayer` module.
+// Attention, softmax and fully connected layer functions of the `myLayer` module.
 //
 // They follow the reference's layer convention (FcForward/FcBackward,
 // Task3/Tinytensor/src/Layers.h:8-26, Layers.cu:9-79): inputs are const
@@ -33,3 +33,24 @@ void AttentionDecode(const TinyTensor<T>& q, const TinyTensor<T>& k_cache, const
 // reference binds it (bind_Layer.cpp:20); output may be input itself.
 template <typename T>
 void SoftmaxForward(const TinyTensor<T>& input, TinyTensor<T>& output);
+
+// Fully connected layer (Layers.cu:9-37): output [.., fout] = input [.., fin]
+// weight [fin, fout] + bias, every leading axis of input a batch axis.  bias
+// is [fout], or [1] for one value added to every output (Layers.cu:28-33).
+// The product runs on the library GEMM (tt_gemm_*, replacing cudaGemm); the
+// bias is added by a rank-1 GEMM of a ones column against the bias row, as the
+// reference does.  float as the reference binds it (bind_Layer.cpp:12-13),
+// and bf16.
+template <typename T>
+void FcForward(const TinyTensor<T>& input, TinyTensor<T>& output, const TinyTensor<T>& weight,
+               const TinyTensor<T>& bias);
+
+// Its gradients (Layers.cu:39-79): grad_input = grad_output weight^T,
+// grad_weight = input^T grad_output, grad_bias = the column sums of
+// grad_output (their total for a [1] bias); each is resized to its operand's
+// shape.  `output` is accepted and not read, as in the reference.
+template <typename T>
+void FcBackward(const TinyTensor<T>& input, const TinyTensor<T>& output, const TinyTensor<T>& weight,
+                const TinyTensor<T>& bias, TinyTensor<T>& grad_input, const TinyTensor<T>& grad_output,
+                TinyTensor<T>& grad_weight, TinyTensor<T>& grad_bias);
+

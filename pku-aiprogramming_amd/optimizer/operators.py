@@ -26,8 +26,9 @@ Design:
 Deliberate departures from the reference: ``matmul(a, b)`` propagates
 gradients (the reference's wraps its arguments in new leaves, :432-433), and
 ``c - t`` computes c - t (the reference aliases ``__rsub__`` to ``__sub__``,
-:187).  The reference's MNIST layers (FC, Conv, MaxPool, the softmax losses,
-:494-665) are not part of this build.
+:187).  Of the reference's MNIST layers, ``FC`` (:498-533) runs on the library
+GEMM through ``myLayer.FcForward`` / ``FcBackward``; Conv, MaxPool and the
+softmax losses (:535-665) are not part of this build.
 """
 from __future__ import annotations
 
@@ -430,6 +431,42 @@ class ReLU(TensorOp):
 
 def relu(a):
     return ReLU()(a)
+
+
+class FC(TensorOp):
+    """Fully connected layer, input @ weight + bias, on the GPU through
+    ``myLayer.FcForward`` / ``FcBackward`` (reference :498-529): weight
+    [fin, fout], bias [fout] or [1]; ``use_bias=False`` zeroes the bias and
+    its gradient as the reference does (:506-507, :527-528).  Every leading
+    axis of the input is a batch axis (the layer's reading, Layers.cu:16-20)."""
+
+    def __init__(self, use_bias: bool = True):
+        self.use_bias = use_bias
+
+    @staticmethod
+    def _dev(a):
+        return Tensor_float(np.asarray(a, np.float32), "gpu")
+
+    def compute(self, input, weight, bias):
+        x, w, b = self._dev(input), self._dev(weight), self._dev(bias)
+        if not self.use_bias:
+            b.zeros()
+        out = Tensor_float([1], "gpu")
+        ml.FcForward(x, out, w, b)
+        return out.numpy()
+
+    def gradient(self, out_grad, node):
+        x, w, b = (self._dev(t.realize_cached_data()) for t in node.inputs)
+        go = self._dev(out_grad.realize_cached_data())
+        gx, gw, gb = Tensor_float([1], "gpu"), Tensor_float([1], "gpu"), Tensor_float([1], "gpu")
+        ml.FcBackward(x, Tensor_float([1], "gpu"), w, b, gx, go, gw, gb)
+        if not self.use_bias:
+            gb.zeros()
+        return Tensor(gx, requires_grad=False), Tensor(gw, requires_grad=False), Tensor(gb, requires_grad=False)
+
+
+def fc(input, weight, bias, use_bias=True):
+    return FC(use_bias)(input, weight, bias)
 
 
 _ATTN_DTYPES = {"float32": Tensor_float, "bf16": Tensor_bf16}

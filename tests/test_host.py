@@ -213,6 +213,12 @@ def test_layer_functions_reject_cpu_tensors(mt):
     x = mt.Tensor_float(np.zeros((4, 10), np.float32), "cpu")
     with pytest.raises(ValueError, match="gpu"):
         myLayer.SoftmaxForward(x, o)
+    w = mt.Tensor_float(np.zeros((10, 3), np.float32), "cpu")
+    bias = mt.Tensor_float(np.zeros(3, np.float32), "cpu")
+    with pytest.raises(ValueError, match="gpu"):
+        myLayer.FcForward(x, o, w, bias)
+    with pytest.raises(ValueError, match="gpu"):
+        myLayer.FcBackward(x, o, w, bias, o, o, o, o)
 
 
 # ------------------------------------------------------------------ autograd layer
