@@ -278,6 +278,22 @@ int tt_gemm_f32(int transa, int transb, int64_t m, int64_t n, int64_t k, float a
 int tt_gemm_bf16(int transa, int transb, int64_t m, int64_t n, int64_t k, float alpha,
                  const uint16_t* A, const uint16_t* B, float beta, uint16_t* C, void* stream);
 
+/* ---------------------------------------------------------------- convolution data movement */
+
+/* im[N][C][H][W] -> col[N][OH*OW][C][kh][kw] with OH = (H + 2 pad_h - kh) /
+ * stride_h + 1 (OW likewise), col[n][oy*OW + ox][c][ky][kx] =
+ * im[n][c][oy stride_h - pad_h + ky][ox stride_w - pad_w + kx] and 0 outside
+ * the image: the reference's im2col (src/Layers.cu:81-119, kernel
+ * src/Layers_kernels.cu:32-66, one launch per batch image), here one launch
+ * for the batch.  dtype TT_F32 or TT_BF16. */
+int tt_im2col(int dtype, const void* im, void* col, int64_t N, int C, int H, int W, int kh, int kw, int pad_h,
+              int pad_w, int stride_h, int stride_w, void* stream);
+/* Its adjoint, the reference's col2im (src/Layers.cu:121-158, kernel
+ * src/Layers_kernels.cu:68-105): im[n][c][y][x] = the sum (in fp32) of the
+ * col entries that im2col fills from it; every element of im is written. */
+int tt_col2im(int dtype, const void* col, void* im, int64_t N, int C, int H, int W, int kh, int kw, int pad_h,
+              int pad_w, int stride_h, int stride_w, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

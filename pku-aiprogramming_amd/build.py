@@ -30,7 +30,7 @@ OBJ = os.path.join(HERE, "_build")
 INCLUDE = os.path.join(ROOT, "include")
 
 HIP_SOURCES = ["tt_runtime.hip", "attn_fwd.hip", "attn_bwd.hip", "attn_bwd_w64.hip", "attn_decode.hip", "softmax.hip",
-               "gemm.hip", "staging.hip"]
+               "gemm.hip", "staging.hip", "conv.hip"]
 # Per-file extra flags.  attn_bwd_w64.hip keeps its dK / dV accumulators in
 # AGPRs by inline asm and needs its builtin MFMAs (scores) to write VGPRs.
 HIP_FILE_FLAGS = {"attn_bwd_w64.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}

@@ -289,6 +289,178 @@ void FcBackward(const TinyTensor<T>& input, const TinyTensor<T>& output, const T
   }
 }
 
+namespace {
+
+struct ConvShape {
+  int64_t batch;
+  int C, H, W;
+};
+
+// The reference's reading of an image tensor (Layers.cu:91-97): the last three
+// axes are C, H, W, the others batch axes.
+ConvShape conv_shape(const std::string& fn, const std::string& name, const std::vector<int>& shape) {
+  if (shape.size() < 3) throw std::invalid_argument(fn + ": " + name + " must have rank >= 3 [.., C, H, W]");
+  ConvShape c{1, shape[shape.size() - 3], shape[shape.size() - 2], shape.back()};
+  for (size_t i = 0; i + 3 < shape.size(); ++i) c.batch *= shape[i];
+  return c;
+}
+
+// Output extent of one axis; throws where the C-ABI would refuse the shape.
+int conv_out(const std::string& fn, int in, int k, int pad, int stride) {
+  if (k < 1 || pad < 0 || stride < 1)
+    throw std::invalid_argument(fn + ": kernel sizes >= 1, pads >= 0 and strides >= 1 required");
+  if ((int64_t)in + 2 * (int64_t)pad < k) throw std::invalid_argument(fn + ": the kernel is larger than the padded image");
+  return (int)((in + 2 * (int64_t)pad - k) / stride + 1);
+}
+
+template <typename T>
+int dtype_code() {
+  return std::is_same<T, float>::value ? TT_F32 : TT_BF16;
+}
+
+template <typename T>
+void im2col_call(const std::string& fn, const T* im, T* col, const ConvShape& s, int kh, int kw, int ph, int pw,
+                 int sh, int sw) {
+  tt_check(tt_im2col(dtype_code<T>(), im, col, s.batch, s.C, s.H, s.W, kh, kw, ph, pw, sh, sw, nullptr),
+           fn.c_str());
+}
+
+template <typename T>
+void col2im_call(const std::string& fn, const T* col, T* im, const ConvShape& s, int kh, int kw, int ph, int pw,
+                 int sh, int sw) {
+  tt_check(tt_col2im(dtype_code<T>(), col, im, s.batch, s.C, s.H, s.W, kh, kw, ph, pw, sh, sw, nullptr),
+           fn.c_str());
+}
+
+}  // namespace
+
+template <typename T>
+void Im2col(const TinyTensor<T>& im_tensor, TinyTensor<T>& col_tensor, const std::vector<int>& kernel_shape,
+            int pad_h, int pad_w, int stride_h, int stride_w) {
+  const std::string fn = "im2col";
+  need_gpu(fn, "im_tensor", im_tensor.device);
+  need_gpu(fn, "col_tensor", col_tensor.device);
+  if (kernel_shape.size() < 2) throw std::invalid_argument(fn + ": kernel_shape must end with [kh, kw]");
+  const ConvShape s = conv_shape(fn, "im_tensor", im_tensor.shape);
+  const int kh = kernel_shape[kernel_shape.size() - 2], kw = kernel_shape.back();
+  const int oh = conv_out(fn, s.H, kh, pad_h, stride_h), ow = conv_out(fn, s.W, kw, pad_w, stride_w);
+  no_alias(fn, {{im_tensor.p_data, "im_tensor"}}, {{col_tensor.p_data, "col_tensor"}});
+  const int P = oh * ow, K = s.C * kh * kw;
+  if (im_tensor.shape.size() == 3)
+    col_tensor.resize(std::vector<int>{P, K});
+  else
+    col_tensor.resize(std::vector<int>{(int)s.batch, P, K});
+  im2col_call(fn, im_tensor.p_data, col_tensor.p_data, s, kh, kw, pad_h, pad_w, stride_h, stride_w);
+  tt_check(tt_sync(), fn.c_str());
+}
+
+template <typename T>
+void Col2im(const TinyTensor<T>& col_tensor, TinyTensor<T>& im_tensor, const std::vector<int>& kernel_shape,
+            const std::vector<int>& im_shape, int pad_h, int pad_w, int stride_h, int stride_w) {
+  const std::string fn = "col2im";
+  need_gpu(fn, "col_tensor", col_tensor.device);
+  need_gpu(fn, "im_tensor", im_tensor.device);
+  if (kernel_shape.size() < 2) throw std::invalid_argument(fn + ": kernel_shape must end with [kh, kw]");
+  const ConvShape s = conv_shape(fn, "im_shape", im_shape);
+  const int kh = kernel_shape[kernel_shape.size() - 2], kw = kernel_shape.back();
+  const int oh = conv_out(fn, s.H, kh, pad_h, stride_h), ow = conv_out(fn, s.W, kw, pad_w, stride_w);
+  if ((int64_t)col_tensor.size != s.batch * oh * ow * (int64_t)s.C * kh * kw)
+    throw std::invalid_argument(fn + ": col_tensor must hold batch x OH*OW x C*kh*kw values");
+  no_alias(fn, {{col_tensor.p_data, "col_tensor"}}, {{im_tensor.p_data, "im_tensor"}});
+  if (im_shape.size() == 3)
+    im_tensor.resize(std::vector<int>{s.C, s.H, s.W});
+  else
+    im_tensor.resize(std::vector<int>{(int)s.batch, s.C, s.H, s.W});
+  col2im_call(fn, col_tensor.p_data, im_tensor.p_data, s, kh, kw, pad_h, pad_w, stride_h, stride_w);
+  tt_check(tt_sync(), fn.c_str());
+}
+
+namespace {
+
+struct ConvDims {
+  ConvShape in;
+  int cout, kh, kw, oh, ow;
+  int64_t P() const { return (int64_t)oh * ow; }
+  int64_t K() const { return (int64_t)in.C * kh * kw; }
+};
+
+template <typename T>
+ConvDims conv_dims(const std::string& fn, const TinyTensor<T>& input, const TinyTensor<T>& weight, int ph, int pw,
+                   int sh, int sw) {
+  need_gpu(fn, "input", input.device);
+  need_gpu(fn, "weight", weight.device);
+  ConvDims d;
+  d.in = conv_shape(fn, "input", input.shape);
+  if (weight.shape.size() != 4) throw std::invalid_argument(fn + ": weight must have rank 4 [Cout, Cin, kh, kw]");
+  if (weight.shape[1] != d.in.C)
+    throw std::invalid_argument(fn + ": weight's Cin (" + std::to_string(weight.shape[1]) +
+                                ") must equal the input's channels (" + std::to_string(d.in.C) + ")");
+  d.cout = weight.shape[0];
+  d.kh = weight.shape[2];
+  d.kw = weight.shape[3];
+  d.oh = conv_out(fn, d.in.H, d.kh, ph, sh);
+  d.ow = conv_out(fn, d.in.W, d.kw, pw, sw);
+  return d;
+}
+
+}  // namespace
+
+template <typename T>
+void ConvForward(const TinyTensor<T>& input, TinyTensor<T>& output, const TinyTensor<T>& weight, int pad_h,
+                 int pad_w, int stride_h, int stride_w) {
+  const std::string fn = "ConvForward";
+  const ConvDims d = conv_dims(fn, input, weight, pad_h, pad_w, stride_h, stride_w);
+  need_gpu(fn, "output", output.device);
+  no_alias(fn, {{input.p_data, "input"}, {weight.p_data, "weight"}}, {{output.p_data, "output"}});
+  std::vector<int> oshape(input.shape.begin(), input.shape.end() - 3);
+  oshape.insert(oshape.end(), {d.cout, d.oh, d.ow});
+  output.resize(oshape);
+  if (d.in.batch == 0 || d.cout == 0) return;
+  const int64_t P = d.P(), K = d.K();
+  TinyTensor<T> col(std::vector<int>{(int)d.in.batch, (int)P, (int)K}, "gpu");
+  im2col_call(fn, input.p_data, col.p_data, d.in, d.kh, d.kw, pad_h, pad_w, stride_h, stride_w);
+  for (int64_t n = 0; n < d.in.batch; ++n)
+    gemm<T>(fn.c_str(), false, true, d.cout, P, K, 1.f, weight.p_data, col.p_data + n * P * K, 0.f,
+            output.p_data + n * d.cout * P);
+  tt_check(tt_sync(), fn.c_str());
+}
+
+template <typename T>
+void ConvBackward(const TinyTensor<T>& input, const TinyTensor<T>& output, const TinyTensor<T>& weight,
+                  TinyTensor<T>& grad_input, const TinyTensor<T>& grad_output, TinyTensor<T>& grad_weight,
+                  int pad_h, int pad_w, int stride_h, int stride_w) {
+  (void)output;
+  const std::string fn = "ConvBackward";
+  const ConvDims d = conv_dims(fn, input, weight, pad_h, pad_w, stride_h, stride_w);
+  need_gpu(fn, "grad_output", grad_output.device);
+  need_gpu(fn, "grad_input", grad_input.device);
+  need_gpu(fn, "grad_weight", grad_weight.device);
+  const int64_t P = d.P(), K = d.K();
+  if ((int64_t)grad_output.size != d.in.batch * d.cout * P)
+    throw std::invalid_argument(fn + ": grad_output must be [.., Cout, OH, OW] with the input's batch axes");
+  no_alias(fn, {{input.p_data, "input"}, {weight.p_data, "weight"}, {grad_output.p_data, "grad_output"}},
+           {{grad_input.p_data, "grad_input"}, {grad_weight.p_data, "grad_weight"}});
+  grad_input.resize(input.shape);
+  grad_weight.resize(weight.shape);
+  if (d.in.batch == 0 || d.cout == 0) {  // sums over nothing
+    grad_input.zeros();
+    grad_weight.zeros();
+    tt_check(tt_sync(), fn.c_str());
+    return;
+  }
+  TinyTensor<T> col(std::vector<int>{(int)d.in.batch, (int)P, (int)K}, "gpu");
+  im2col_call(fn, input.p_data, col.p_data, d.in, d.kh, d.kw, pad_h, pad_w, stride_h, stride_w);
+  TinyTensor<T> grad_col(std::vector<int>{(int)d.in.batch, (int)P, (int)K}, "gpu");
+  for (int64_t n = 0; n < d.in.batch; ++n) {
+    const T* go = grad_output.p_data + n * d.cout * P;
+    gemm<T>(fn.c_str(), false, false, d.cout, K, P, 1.f, go, col.p_data + n * P * K, n == 0 ? 0.f : 1.f,
+            grad_weight.p_data);
+    gemm<T>(fn.c_str(), true, false, P, K, d.cout, 1.f, go, weight.p_data, 0.f, grad_col.p_data + n * P * K);
+  }
+  col2im_call(fn, grad_col.p_data, grad_input.p_data, d.in, d.kh, d.kw, pad_h, pad_w, stride_h, stride_w);
+  tt_check(tt_sync(), fn.c_str());
+}
+
 template void AttentionForward<float>(const TinyTensor<float>&, const TinyTensor<float>&, const TinyTensor<float>&,
                                       TinyTensor<float>&, TinyTensor<float>&, float, bool);
 template void AttentionForward<bf16>(const TinyTensor<bf16>&, const TinyTensor<bf16>&, const TinyTensor<bf16>&,
@@ -314,3 +486,19 @@ template void FcBackward<float>(const TinyTensor<float>&, const TinyTensor<float
 template void FcBackward<bf16>(const TinyTensor<bf16>&, const TinyTensor<bf16>&, const TinyTensor<bf16>&,
                                const TinyTensor<bf16>&, TinyTensor<bf16>&, const TinyTensor<bf16>&,
                                TinyTensor<bf16>&, TinyTensor<bf16>&);
+template void Im2col<float>(const TinyTensor<float>&, TinyTensor<float>&, const std::vector<int>&, int, int, int,
+                            int);
+template void Im2col<bf16>(const TinyTensor<bf16>&, TinyTensor<bf16>&, const std::vector<int>&, int, int, int, int);
+template void Col2im<float>(const TinyTensor<float>&, TinyTensor<float>&, const std::vector<int>&,
+                            const std::vector<int>&, int, int, int, int);
+template void Col2im<bf16>(const TinyTensor<bf16>&, TinyTensor<bf16>&, const std::vector<int>&,
+                           const std::vector<int>&, int, int, int, int);
+template void ConvForward<float>(const TinyTensor<float>&, TinyTensor<float>&, const TinyTensor<float>&, int, int,
+                                 int, int);
+template void ConvForward<bf16>(const TinyTensor<bf16>&, TinyTensor<bf16>&, const TinyTensor<bf16>&, int, int, int,
+                                int);
+template void ConvBackward<float>(const TinyTensor<float>&, const TinyTensor<float>&, const TinyTensor<float>&,
+                                  TinyTensor<float>&, const TinyTensor<float>&, TinyTensor<float>&, int, int, int,
+                                  int);
+template void ConvBackward<bf16>(const TinyTensor<bf16>&, const TinyTensor<bf16>&, const TinyTensor<bf16>&,
+                                 TinyTensor<bf16>&, const TinyTensor<bf16>&, TinyTensor<bf16>&, int, int, int, int);

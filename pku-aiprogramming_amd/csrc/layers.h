@@ -34,7 +34,7 @@ void AttentionDecode(const TinyTensor<T>& q, const TinyTensor<T>& k_cache, const
 template <typename T>
 void SoftmaxForward(const TinyTensor<T>& input, TinyTensor<T>& output);
 
-// Fully connected layer (Layers.cu:9-37): output [.., fout] = input [.., fin]
+// Fully connected layer (Layers.cu:9-39): output [.., fout] = input [.., fin]
 // weight [fin, fout] + bias, every leading axis of input a batch axis.  bias
 // is [fout], or [1] for one value added to every output (Layers.cu:28-33).
 // The product runs on the library GEMM (tt_gemm_*, replacing cudaGemm); the
@@ -45,7 +45,7 @@ template <typename T>
 void FcForward(const TinyTensor<T>& input, TinyTensor<T>& output, const TinyTensor<T>& weight,
                const TinyTensor<T>& bias);
 
-// Its gradients (Layers.cu:39-79): grad_input = grad_output weight^T,
+// Its gradients (Layers.cu:41-79): grad_input = grad_output weight^T,
 // grad_weight = input^T grad_output, grad_bias = the column sums of
 // grad_output (their total for a [1] bias); each is resized to its operand's
 // shape.  `output` is accepted and not read, as in the reference.
@@ -53,4 +53,32 @@ template <typename T>
 void FcBackward(const TinyTensor<T>& input, const TinyTensor<T>& output, const TinyTensor<T>& weight,
                 const TinyTensor<T>& bias, TinyTensor<T>& grad_input, const TinyTensor<T>& grad_output,
                 TinyTensor<T>& grad_weight, TinyTensor<T>& grad_bias);
+
+// Convolution data movement (Layers.cu:81-158): im [.., C, H, W] to its
+// column matrix [P, C kh kw] (rank-3 image) or [batch, P, C kh kw], P = OH OW
+// output pixels, and col2im, its adjoint, back to im_shape (each image
+// element the sum of the column entries read from it).  kernel_shape's last
+// two entries are kh, kw.
+template <typename T>
+void Im2col(const TinyTensor<T>& im_tensor, TinyTensor<T>& col_tensor, const std::vector<int>& kernel_shape,
+            int pad_h, int pad_w, int stride_h, int stride_w);
+template <typename T>
+void Col2im(const TinyTensor<T>& col_tensor, TinyTensor<T>& im_tensor, const std::vector<int>& kernel_shape,
+            const std::vector<int>& im_shape, int pad_h, int pad_w, int stride_h, int stride_w);
+
+// Convolution layer (Layers.cu:160-200): input [.., Cin, H, W], weight
+// [Cout, Cin, kh, kw] -> output [.., Cout, OH, OW]: one im2col launch for the
+// batch, then per image output = weight (as [Cout, Cin kh kw]) col^T on the
+// library GEMM.  No bias, as in the reference.
+template <typename T>
+void ConvForward(const TinyTensor<T>& input, TinyTensor<T>& output, const TinyTensor<T>& weight, int pad_h,
+                 int pad_w, int stride_h, int stride_w);
+
+// Its gradients (Layers.cu:202-252): grad_weight = sum over images of
+// grad_output col (GEMM, accumulating), grad_col = grad_output^T weight per
+// image, grad_input = col2im(grad_col).  `output` is accepted and not read.
+template <typename T>
+void ConvBackward(const TinyTensor<T>& input, const TinyTensor<T>& output, const TinyTensor<T>& weight,
+                  TinyTensor<T>& grad_input, const TinyTensor<T>& grad_output, TinyTensor<T>& grad_weight,
+                  int pad_h, int pad_w, int stride_h, int stride_w);
 

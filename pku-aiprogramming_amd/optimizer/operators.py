@@ -27,8 +27,9 @@ Deliberate departures from the reference: ``matmul(a, b)`` propagates
 gradients (the reference's wraps its arguments in new leaves, :432-433), and
 ``c - t`` computes c - t (the reference aliases ``__rsub__`` to ``__sub__``,
 :187).  Of the reference's MNIST layers, ``FC`` (:498-533) runs on the library
-GEMM through ``myLayer.FcForward`` / ``FcBackward``; Conv, MaxPool and the
-softmax losses (:535-665) are not part of this build.
+GEMM through ``myLayer.FcForward`` / ``FcBackward`` and ``Conv`` (:535-569)
+through ``myLayer.ConvForward`` / ``ConvBackward`` (im2col + the GEMM); MaxPool
+and the softmax losses (:570-665) are not part of this build.
 """
 from __future__ import annotations
 
@@ -467,6 +468,36 @@ class FC(TensorOp):
 
 def fc(input, weight, bias, use_bias=True):
     return FC(use_bias)(input, weight, bias)
+
+
+class Conv(TensorOp):
+    """2-D convolution, no bias, on the GPU through ``myLayer.ConvForward`` /
+    ``ConvBackward`` (reference :535-566): input [N, Cin, H, W], weight
+    [Cout, Cin, kh, kw] -> [N, Cout, OH, OW], OH = (H + 2 pad_h - kh) //
+    stride_h + 1; ``gradient`` returns (grad_input, grad_weight)."""
+
+    def __init__(self, pad_h, pad_w, stride_h, stride_w):
+        self.pad_h, self.pad_w, self.stride_h, self.stride_w = pad_h, pad_w, stride_h, stride_w
+
+    def _args(self):
+        return self.pad_h, self.pad_w, self.stride_h, self.stride_w
+
+    def compute(self, input, weight):
+        x, w = FC._dev(input), FC._dev(weight)
+        out = Tensor_float([1], "gpu")
+        ml.ConvForward(x, out, w, *self._args())
+        return out.numpy()
+
+    def gradient(self, out_grad, node):
+        x, w = (FC._dev(t.realize_cached_data()) for t in node.inputs)
+        go = FC._dev(out_grad.realize_cached_data())
+        gx, gw = Tensor_float([1], "gpu"), Tensor_float([1], "gpu")
+        ml.ConvBackward(x, Tensor_float([1], "gpu"), w, gx, go, gw, *self._args())
+        return Tensor(gx, requires_grad=False), Tensor(gw, requires_grad=False)
+
+
+def conv(input, weight, pad_h=0, pad_w=0, stride_h=1, stride_w=1):
+    return Conv(pad_h, pad_w, stride_h, stride_w)(input, weight)
 
 
 _ATTN_DTYPES = {"float32": Tensor_float, "bf16": Tensor_bf16}
