@@ -263,6 +263,18 @@ int tt_attn_decode_f32(const float* q, const float* k, const float* v, float* o,
  * +inf or NaN) gives NaN, as the reference's x - max does. */
 int tt_softmax_rows_f32(const float* x, float* y, int64_t rows, int64_t cols, void* stream);
 
+/* loss[0] = sum over rows i of -log p[i][labels[i]] for softmax rows p
+ * [rows x cols] and int labels: the reference's CrossEntropyLoss
+ * (src/Layers.cu:383-404; kernel src/Layers_kernels.cu:260-270, then a
+ * thrust sum), in double, in a fixed order.  A label outside [0, cols) gives
+ * NaN.  The caller synchronizes before reading loss. */
+int tt_cross_entropy_f32(const float* p, const int* labels, float* loss, int64_t rows, int64_t cols, void* stream);
+/* grad = p - onehot(labels) (rows x cols), the reference's
+ * CrossEntropyLossBackward (src/Layers.cu:406-423); a label outside [0, cols)
+ * subtracts nothing.  grad may alias p. */
+int tt_cross_entropy_backward_f32(const float* p, const int* labels, float* grad, int64_t rows, int64_t cols,
+                                  void* stream);
+
 /* ---------------------------------------------------------------- GEMM */
 
 /* C = alpha op(A) op(B) + beta C, all row-major: op(A) is m x k, op(B) is

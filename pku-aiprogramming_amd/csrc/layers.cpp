@@ -461,6 +461,69 @@ void ConvBackward(const TinyTensor<T>& input, const TinyTensor<T>& output, const
   tt_check(tt_sync(), fn.c_str());
 }
 
+namespace {
+
+// rows x classes of a softmax output, and its labels' count checked
+template <typename T>
+std::pair<int64_t, int64_t> ce_dims(const std::string& fn, const TinyTensor<T>& p, const TinyTensor<int>& labels) {
+  if (p.shape.empty()) throw std::invalid_argument(fn + ": the softmax output must have rank >= 1");
+  int64_t rows = 1;
+  for (size_t i = 0; i + 1 < p.shape.size(); ++i) rows *= p.shape[i];
+  if ((int64_t)labels.size != rows)
+    throw std::invalid_argument(fn + ": labels must hold one class per row (" + std::to_string(rows) + ")");
+  return {rows, (int64_t)p.shape.back()};
+}
+
+}  // namespace
+
+template <typename T>
+float SoftmaxLoss(const TinyTensor<T>& softmax_output, const TinyTensor<int>& labels) {
+  static_assert(std::is_same<T, float>::value, "SoftmaxLoss is float only, as in the reference");
+  const std::string fn = "SoftmaxLoss";
+  const auto [rows, cols] = ce_dims(fn, softmax_output, labels);
+  if (rows == 0) return 0.f;
+  const std::vector<float> p = softmax_output.get_data();
+  const std::vector<int> lab = labels.get_data();
+  int64_t wrong = 0;
+  for (int64_t i = 0; i < rows; ++i) {
+    int64_t best = 0;
+    for (int64_t j = 1; j < cols; ++j)
+      if (p[i * cols + j] > p[i * cols + best]) best = j;
+    wrong += best != lab[i];
+  }
+  return (float)wrong / (float)rows;
+}
+
+template <typename T>
+void CrossEntropyLoss(const TinyTensor<T>& input, const TinyTensor<int>& labels, TinyTensor<T>& loss) {
+  static_assert(std::is_same<T, float>::value, "CrossEntropyLoss is float only, as in the reference");
+  const std::string fn = "CrossEntropyLoss";
+  need_gpu(fn, "input", input.device);
+  need_gpu(fn, "labels", labels.device);
+  need_gpu(fn, "loss", loss.device);
+  const auto [rows, cols] = ce_dims(fn, input, labels);
+  no_alias(fn, {{input.p_data, "input"}}, {{loss.p_data, "loss"}});
+  loss.resize(std::vector<int>{1});
+  tt_check(tt_cross_entropy_f32(input.p_data, labels.p_data, loss.p_data, rows, cols, nullptr), fn.c_str());
+  tt_check(tt_sync(), fn.c_str());
+}
+
+template <typename T>
+void CrossEntropyLossBackward(const TinyTensor<T>& softmax_output, const TinyTensor<int>& labels,
+                              TinyTensor<T>& grad_input) {
+  static_assert(std::is_same<T, float>::value, "CrossEntropyLossBackward is float only, as in the reference");
+  const std::string fn = "CrossEntropyLossBackward";
+  need_gpu(fn, "softmax_output", softmax_output.device);
+  need_gpu(fn, "labels", labels.device);
+  need_gpu(fn, "grad_input", grad_input.device);
+  const auto [rows, cols] = ce_dims(fn, softmax_output, labels);
+  if (&grad_input != &softmax_output) grad_input.resize(softmax_output.shape);
+  tt_check(tt_cross_entropy_backward_f32(softmax_output.p_data, labels.p_data, grad_input.p_data, rows, cols,
+                                         nullptr),
+           fn.c_str());
+  tt_check(tt_sync(), fn.c_str());
+}
+
 template void AttentionForward<float>(const TinyTensor<float>&, const TinyTensor<float>&, const TinyTensor<float>&,
                                       TinyTensor<float>&, TinyTensor<float>&, float, bool);
 template void AttentionForward<bf16>(const TinyTensor<bf16>&, const TinyTensor<bf16>&, const TinyTensor<bf16>&,
@@ -502,3 +565,6 @@ template void ConvBackward<float>(const TinyTensor<float>&, const TinyTensor<flo
                                   int);
 template void ConvBackward<bf16>(const TinyTensor<bf16>&, const TinyTensor<bf16>&, const TinyTensor<bf16>&,
                                  TinyTensor<bf16>&, const TinyTensor<bf16>&, TinyTensor<bf16>&, int, int, int, int);
+template float SoftmaxLoss<float>(const TinyTensor<float>&, const TinyTensor<int>&);
+template void CrossEntropyLoss<float>(const TinyTensor<float>&, const TinyTensor<int>&, TinyTensor<float>&);
+template void CrossEntropyLossBackward<float>(const TinyTensor<float>&, const TinyTensor<int>&, TinyTensor<float>&);

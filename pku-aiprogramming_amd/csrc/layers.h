@@ -82,3 +82,18 @@ void ConvBackward(const TinyTensor<T>& input, const TinyTensor<T>& output, const
                   TinyTensor<T>& grad_input, const TinyTensor<T>& grad_output, TinyTensor<T>& grad_weight,
                   int pad_h, int pad_w, int stride_h, int stride_w);
 
+// Softmax cross-entropy after SoftmaxForward (Layers.cu:351-423), float as the
+// reference binds them (bind_Layer.cpp:21-23).  input / softmax_output are
+// softmax rows [.., classes], labels int [rows] on the "gpu" device.
+// SoftmaxLoss: the fraction of rows whose first largest entry is not the
+// label (computed on the host, as in the reference).  CrossEntropyLoss: loss
+// [1] = sum of -log p[label] over the rows.  CrossEntropyLossBackward:
+// grad_input = softmax_output - onehot(labels).
+template <typename T>
+float SoftmaxLoss(const TinyTensor<T>& softmax_output, const TinyTensor<int>& labels);
+template <typename T>
+void CrossEntropyLoss(const TinyTensor<T>& input, const TinyTensor<int>& labels, TinyTensor<T>& loss);
+template <typename T>
+void CrossEntropyLossBackward(const TinyTensor<T>& softmax_output, const TinyTensor<int>& labels,
+                              TinyTensor<T>& grad_input);
+

@@ -414,3 +414,78 @@ extern "C" int tt_softmax_rows_f32(const float* x, float* y, int64_t rows, int64
   TT_LAUNCHED("tt_softmax_rows_f32", s);
   return ok();
 }
+
+// ---------------------------------------------------------------- cross-entropy on softmax rows
+// The loss and gradient that follow SoftmaxForward in the reference's
+// softmax cross-entropy (src/Layers.cu:383-423, kernels
+// src/Layers_kernels.cu:260-282): loss = sum_i -log p[i][label_i], and
+// grad = p - onehot(label).  A label outside [0, cols) makes its row's loss
+// term NaN and subtracts nothing from its gradient row (the reference reads
+// out of bounds there).
+namespace tt {
+namespace {
+
+constexpr int kCeThreads = 1024;
+
+// One workgroup: each thread sums the rows t, t + 1024, ... in double, then a
+// fixed-order tree over the workgroup, so the result does not depend on
+// timing.
+__global__ __launch_bounds__(kCeThreads) void k_ce_loss(const float* __restrict__ p, const int* __restrict__ labels,
+                                                        float* __restrict__ loss, int64_t rows, int64_t cols) {
+  __shared__ double part[kCeThreads];
+  double acc = 0.0;
+  for (int64_t i = threadIdx.x; i < rows; i += kCeThreads) {
+    const int lab = labels[i];
+    acc += (lab >= 0 && lab < cols) ? -log((double)p[i * cols + lab]) : (double)NAN;
+  }
+  part[threadIdx.x] = acc;
+  __syncthreads();
+  for (int w = kCeThreads / 2; w > 0; w >>= 1) {
+    if ((int)threadIdx.x < w) part[threadIdx.x] += part[threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) loss[0] = (float)part[0];
+}
+
+__global__ __launch_bounds__(256) void k_ce_backward(const float* __restrict__ p, const int* __restrict__ labels,
+                                                     float* __restrict__ grad, int64_t rows, int64_t cols) {
+  const int64_t n = rows * cols;
+  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < n; e += (int64_t)gridDim.x * 256) {
+    const int64_t i = e / cols, j = e - i * cols;
+    grad[e] = p[e] - (labels[i] == j ? 1.f : 0.f);
+  }
+}
+
+}  // namespace
+}  // namespace tt
+
+extern "C" int tt_cross_entropy_f32(const float* p, const int* labels, float* loss, int64_t rows, int64_t cols,
+                                    void* stream) {
+  using namespace tt;
+  if (rows < 0 || cols < 0) return fail(TT_ERR_ARG, "tt_cross_entropy_f32: negative size");
+  if (!loss || (rows > 0 && (!p || !labels || cols == 0)))
+    return fail(TT_ERR_ARG, "tt_cross_entropy_f32: null pointer or no columns");
+  int rc = ensure_init();
+  if (rc) return rc;
+  hipStream_t s = stream_or_default(stream);
+  hipLaunchKernelGGL(k_ce_loss, dim3(1), dim3(kCeThreads), 0, s, p, labels, loss, rows, cols);
+  TT_LAUNCHED("tt_cross_entropy_f32", s);
+  return ok();
+}
+
+extern "C" int tt_cross_entropy_backward_f32(const float* p, const int* labels, float* grad, int64_t rows,
+                                             int64_t cols, void* stream) {
+  using namespace tt;
+  if (rows < 0 || cols < 0) return fail(TT_ERR_ARG, "tt_cross_entropy_backward_f32: negative size");
+  if (rows == 0 || cols == 0) return ok();
+  if (!p || !labels || !grad) return fail(TT_ERR_ARG, "tt_cross_entropy_backward_f32: null pointer");
+  int rc = ensure_init();
+  if (rc) return rc;
+  hipStream_t s = stream_or_default(stream);
+  int64_t blocks = (rows * cols + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  hipLaunchKernelGGL(k_ce_backward, dim3((unsigned)blocks), dim3(256), 0, s, p, labels, grad, rows, cols);
+  TT_LAUNCHED("tt_cross_entropy_backward_f32", s);
+  return ok();
+}
+

@@ -28,8 +28,9 @@ gradients (the reference's wraps its arguments in new leaves, :432-433), and
 ``c - t`` computes c - t (the reference aliases ``__rsub__`` to ``__sub__``,
 :187).  Of the reference's MNIST layers, ``FC`` (:498-533) runs on the library
 GEMM through ``myLayer.FcForward`` / ``FcBackward`` and ``Conv`` (:535-569)
-through ``myLayer.ConvForward`` / ``ConvBackward`` (im2col + the GEMM); MaxPool
-and the softmax losses (:570-665) are not part of this build.
+through ``myLayer.ConvForward`` / ``ConvBackward`` (im2col + the GEMM), and the
+softmax losses (:604-665) through ``myLayer.SoftmaxForward`` and the
+cross-entropy kernels; MaxPool (:570-602) is not part of this build.
 """
 from __future__ import annotations
 
@@ -498,6 +499,84 @@ class Conv(TensorOp):
 
 def conv(input, weight, pad_h=0, pad_w=0, stride_h=1, stride_w=1):
     return Conv(pad_h, pad_w, stride_h, stride_w)(input, weight)
+
+
+def _labels_array(labels) -> np.ndarray:
+    data = labels.realize_cached_data() if isinstance(labels, Value) else labels
+    return np.asarray(data).astype(np.int32).ravel()
+
+
+class _SoftmaxLossBase(TensorOp):
+    """Softmax over the classes of logits [batch, classes], then (loss, error)
+    as the reference reports them (operators.py:604-665): the summed cross
+    entropy and the misclassified rows, both divided by 10 * batch (the
+    reference's reporting scale), returned as a 2-element float64 array so
+    that ``loss, error = node.realize_cached_data()`` unpacks as before and
+    ``node.backward()`` works.  The gradient with respect to the logits is
+    (softmax - onehot(labels)) / batch, whatever out_grad holds (as in the
+    reference)."""
+
+    def __init__(self, labels):
+        self.labels = _labels_array(labels)
+        self.batchsize = self.labels.shape[0]
+        self.softmax = None
+
+    def _report(self, loss_sum):
+        wrong = np.count_nonzero(self.softmax.argmax(axis=1) != self.labels)
+        scale = 10.0 * self.batchsize
+        return np.array([loss_sum / scale, wrong / scale])
+
+
+class Softmaxloss(_SoftmaxLossBase):
+    """The reference's CPU softmax loss (operators.py:604-629), in numpy."""
+
+    def compute(self, z):
+        z = np.asarray(z, np.float64)
+        shifted = z - z.max(axis=1, keepdims=True)
+        e = np.exp(shifted)
+        self.softmax = e / e.sum(axis=1, keepdims=True)
+        rows = np.arange(self.batchsize)
+        # -log softmax[label] = log sum_j exp(z_j - z_label)
+        loss_sum = np.log(np.exp(shifted - shifted[rows, self.labels][:, None]).sum(axis=1)).sum()
+        return self._report(loss_sum)
+
+    def gradient(self, out_grad, node):
+        g = self.softmax.copy()
+        g[np.arange(self.batchsize), self.labels] -= 1.0
+        return Tensor(g / self.batchsize, requires_grad=False)
+
+
+class Softmaxcrossentropyloss(_SoftmaxLossBase):
+    """The reference's GPU softmax cross entropy (operators.py:636-661):
+    ``myLayer.SoftmaxForward``, ``CrossEntropyLoss`` and, for the gradient,
+    ``CrossEntropyLossBackward`` scaled by 1 / batch."""
+
+    def _labels_dev(self):
+        return Tensor_int(self.labels.reshape(1, -1), "gpu")
+
+    def compute(self, input):
+        x = Tensor_float(np.asarray(input, np.float32), "gpu")
+        p = Tensor_float([1], "gpu")
+        ml.SoftmaxForward(x, p)
+        self.softmax = np.asarray(p.numpy()).reshape(x.get_shape())
+        loss = Tensor_float([1], "gpu")
+        ml.CrossEntropyLoss(p, self._labels_dev(), loss)
+        return self._report(float(loss.get_data()[0]))
+
+    def gradient(self, out_grad, node):
+        p = Tensor_float(self.softmax.astype(np.float32), "gpu")
+        g = Tensor_float([1], "gpu")
+        ml.CrossEntropyLossBackward(p, self._labels_dev(), g)
+        g.mults(1.0 / self.batchsize)
+        return Tensor(g, requires_grad=False)
+
+
+def softmaxloss(X, y):
+    return Softmaxloss(y)(X)
+
+
+def softmaxcrossentropyloss(X, y):
+    return Softmaxcrossentropyloss(y)(X)
 
 
 _ATTN_DTYPES = {"float32": Tensor_float, "bf16": Tensor_bf16}
