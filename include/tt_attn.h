@@ -306,6 +306,20 @@ int tt_im2col(int dtype, const void* im, void* col, int64_t N, int C, int H, int
 int tt_col2im(int dtype, const void* col, void* im, int64_t N, int C, int H, int W, int kh, int kw, int pad_h,
               int pad_w, int stride_h, int stride_w, void* stream);
 
+/* Max pooling over `planes` images [H][W] (batch x channels): out and mask
+ * [planes][OH][OW] (OH, OW as for im2col); the window is clipped to the
+ * image, the first largest entry in row-major order wins, mask holds its index
+ * y * W + x as a float (-1, out -FLT_MAX, for a window with no image element):
+ * the reference's MaxPoolingForward (src/Layers.cu:254-286, kernel
+ * src/Layers_kernels.cu:109-153). */
+int tt_maxpool_f32(const float* in, float* out, float* mask, int64_t planes, int H, int W, int kh, int kw, int pad_h,
+                   int pad_w, int stride_h, int stride_w, void* stream);
+/* grad_in [planes][H][W] = the sum of grad_out over the windows whose mask
+ * points at each element (MaxPoolingBackward, src/Layers.cu:288-322, assigns
+ * instead: equal for non-overlapping windows); every element is written. */
+int tt_maxpool_backward_f32(const float* grad_out, const float* mask, float* grad_in, int64_t planes, int H, int W,
+                            int kh, int kw, int pad_h, int pad_w, int stride_h, int stride_w, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

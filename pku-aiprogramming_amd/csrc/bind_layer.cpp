@@ -1,4 +1,4 @@
-// Module `myLayer`: the attention entry points, SoftmaxForward with its cross-entropy, FC and convolution, bound in the style of
+// Module `myLayer`: the attention entry points, SoftmaxForward with its cross-entropy, FC, convolution and max pooling, bound in the style of
 // Task3/Tinytensor/src/bind_Layer.cpp:10-24 (free functions over TinyTensor
 // references), with float and bf16 overloads.
 #include <pybind11/pybind11.h>
@@ -36,6 +36,11 @@ PYBIND11_MODULE(myLayer, m) {
         py::arg("grad_input"), py::arg("grad_output"), py::arg("grad_weight"), py::arg("grad_bias"));
   m.def("FcBackward", &FcBackward<bf16>, py::arg("input"), py::arg("output"), py::arg("weight"), py::arg("bias"),
         py::arg("grad_input"), py::arg("grad_output"), py::arg("grad_weight"), py::arg("grad_bias"));
+  m.def("MaxPoolingForward", &MaxPoolingForward<float>, py::arg("input"), py::arg("output"), py::arg("mask"),
+        py::arg("kernel_shape"), py::arg("pad_h"), py::arg("pad_w"), py::arg("stride_h"), py::arg("stride_w"));
+  m.def("MaxPoolingBackward", &MaxPoolingBackward<float>, py::arg("grad_output"), py::arg("mask"),
+        py::arg("grad_input"), py::arg("input_shape"), py::arg("kernel_shape"), py::arg("pad_h"), py::arg("pad_w"),
+        py::arg("stride_h"), py::arg("stride_w"));
   // float, positional, as the reference binds them (bind_Layer.cpp:21-23)
   m.def("SoftmaxLoss", &SoftmaxLoss<float>, py::arg("softmax_output"), py::arg("labels"));
   m.def("CrossEntropyLoss", &CrossEntropyLoss<float>, py::arg("input"), py::arg("labels"), py::arg("loss"));

@@ -92,6 +92,60 @@ __global__ __launch_bounds__(256) void k_col2im(const T* __restrict__ col, T* __
   }
 }
 
+// Max pooling (reference src/Layers.cu:254-322, kernels
+// src/Layers_kernels.cu:109-175): one thread per output element; the window
+// is clipped to the image (padding never wins), the first largest entry in
+// row-major order is kept, and mask holds its index y * W + x in the (n, c)
+// plane as a float (-1, and -FLT_MAX out, for a window with no image element).
+__global__ __launch_bounds__(256) void k_maxpool(const float* __restrict__ in, float* __restrict__ out,
+                                                 float* __restrict__ mask, int64_t total, ConvGeom g) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+    const int ox = (int)(i % g.ow), oy = (int)((i / g.ow) % g.oh);
+    const int64_t plane = i / ((int64_t)g.oh * g.ow);
+    const int y0 = oy * g.sh - g.ph, x0 = ox * g.sw - g.pw;
+    const int y1 = min(y0 + g.kh, g.H), x1 = min(x0 + g.kw, g.W);
+    const float* pl = in + plane * g.H * g.W;
+    float best = -3.402823466e38f;
+    int arg = -1;
+    for (int y = max(y0, 0); y < y1; ++y)
+      for (int x = max(x0, 0); x < x1; ++x)
+        if (pl[y * g.W + x] > best) {
+          best = pl[y * g.W + x];
+          arg = y * g.W + x;
+        }
+    out[i] = best;
+    mask[i] = (float)arg;
+  }
+}
+
+// Its gradient, one thread per input element: the sum of grad_out over the
+// windows whose mask points at this element (the reference assigns instead,
+// which with overlapping windows keeps one of them, whichever thread writes
+// last; with non-overlapping windows the two agree).
+__global__ __launch_bounds__(256) void k_maxpool_backward(const float* __restrict__ gout,
+                                                          const float* __restrict__ mask,
+                                                          float* __restrict__ gin, int64_t total, ConvGeom g) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+    const int x = (int)(i % g.W), y = (int)((i / g.W) % g.H);
+    const int64_t plane = i / ((int64_t)g.H * g.W);
+    const float* gp = gout + plane * g.oh * g.ow;
+    const float* mp = mask + plane * g.oh * g.ow;
+    const float self = (float)(y * g.W + x);
+    float s = 0.f;
+    for (int ky = 0; ky < g.kh; ++ky) {
+      const int ty = y + g.ph - ky;
+      if (ty < 0 || ty % g.sh != 0 || ty / g.sh >= g.oh) continue;
+      for (int kx = 0; kx < g.kw; ++kx) {
+        const int tx = x + g.pw - kx;
+        if (tx < 0 || tx % g.sw != 0 || tx / g.sw >= g.ow) continue;
+        const int o = (ty / g.sh) * g.ow + tx / g.sw;
+        if (mp[o] == self) s += gp[o];
+      }
+    }
+    gin[i] = s;
+  }
+}
+
 int conv_geom(const char* fn, int64_t N, int C, int H, int W, int kh, int kw, int ph, int pw, int sh, int sw,
               ConvGeom& g) {
   if (N < 0 || C < 1 || H < 1 || W < 1 || kh < 1 || kw < 1)
@@ -150,3 +204,46 @@ extern "C" int tt_col2im(int dtype, const void* col, void* im, int64_t N, int C,
   return conv_entry<false>("tt_col2im", dtype, col, im, N, C, H, W, kh, kw, pad_h, pad_w, stride_h, stride_w,
                            stream);
 }
+
+namespace tt {
+namespace {
+
+// backward: (a, b, c) = (grad_out, mask, grad_in); forward: (in, out, mask).
+int pool_launch(const char* fn, bool backward, const float* a, float* b, float* c, int64_t planes, int H, int W,
+                int kh, int kw, int ph, int pw, int sh, int sw, void* stream) {
+  ConvGeom g;
+  int rc = conv_geom(fn, planes, 1, H, W, kh, kw, ph, pw, sh, sw, g);
+  if (rc) return rc;
+  const int64_t total = backward ? planes * (int64_t)H * W : planes * (int64_t)g.oh * g.ow;
+  if (total == 0) return ok();
+  if (!a || !b || !c) return fail(TT_ERR_ARG, std::string(fn) + ": null pointer");
+  rc = ensure_init();
+  if (rc) return rc;
+  hipStream_t s = stream_or_default(stream);
+  int64_t blocks = (total + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  if (backward)
+    hipLaunchKernelGGL(k_maxpool_backward, dim3((unsigned)blocks), dim3(256), 0, s, a, b, c, total, g);
+  else
+    hipLaunchKernelGGL(k_maxpool, dim3((unsigned)blocks), dim3(256), 0, s, a, b, c, total, g);
+  TT_LAUNCHED(fn, s);
+  return ok();
+}
+
+}  // namespace
+}  // namespace tt
+
+extern "C" int tt_maxpool_f32(const float* in, float* out, float* mask, int64_t planes, int H, int W, int kh,
+                              int kw, int pad_h, int pad_w, int stride_h, int stride_w, void* stream) {
+  return tt::pool_launch("tt_maxpool_f32", false, in, out, mask, planes, H, W, kh, kw, pad_h, pad_w, stride_h,
+                         stride_w, stream);
+}
+
+extern "C" int tt_maxpool_backward_f32(const float* grad_out, const float* mask, float* grad_in, int64_t planes,
+                                       int H, int W, int kh, int kw, int pad_h, int pad_w, int stride_h,
+                                       int stride_w, void* stream) {
+  // the mask is only read; the helper's middle pointer is writable for the forward's output
+  return tt::pool_launch("tt_maxpool_backward_f32", true, grad_out, const_cast<float*>(mask), grad_in, planes, H, W,
+                         kh, kw, pad_h, pad_w, stride_h, stride_w, stream);
+}
+

@@ -524,6 +524,57 @@ void CrossEntropyLossBackward(const TinyTensor<T>& softmax_output, const TinyTen
   tt_check(tt_sync(), fn.c_str());
 }
 
+template <typename T>
+void MaxPoolingForward(const TinyTensor<T>& input, TinyTensor<T>& output, TinyTensor<T>& mask,
+                       const std::vector<int>& kernel_shape, int pad_h, int pad_w, int stride_h, int stride_w) {
+  static_assert(std::is_same<T, float>::value, "MaxPoolingForward is float only, as in the reference");
+  const std::string fn = "MaxPoolingForward";
+  need_gpu(fn, "input", input.device);
+  need_gpu(fn, "output", output.device);
+  need_gpu(fn, "mask", mask.device);
+  if (kernel_shape.size() < 2) throw std::invalid_argument(fn + ": kernel_shape must end with [kh, kw]");
+  const ConvShape s = conv_shape(fn, "input", input.shape);
+  const int kh = kernel_shape[kernel_shape.size() - 2], kw = kernel_shape.back();
+  const int oh = conv_out(fn, s.H, kh, pad_h, stride_h), ow = conv_out(fn, s.W, kw, pad_w, stride_w);
+  no_alias(fn, {{input.p_data, "input"}}, {{output.p_data, "output"}, {mask.p_data, "mask"}});
+  std::vector<int> oshape(input.shape.begin(), input.shape.end() - 2);
+  oshape.insert(oshape.end(), {oh, ow});
+  output.resize(oshape);
+  mask.resize(oshape);
+  tt_check(tt_maxpool_f32(input.p_data, output.p_data, mask.p_data, s.batch * s.C, s.H, s.W, kh, kw, pad_h, pad_w,
+                          stride_h, stride_w, nullptr),
+           fn.c_str());
+  tt_check(tt_sync(), fn.c_str());
+}
+
+template <typename T>
+void MaxPoolingBackward(const TinyTensor<T>& grad_output, const TinyTensor<T>& mask, TinyTensor<T>& grad_input,
+                        const std::vector<int>& input_shape, const std::vector<int>& kernel_shape, int pad_h,
+                        int pad_w, int stride_h, int stride_w) {
+  static_assert(std::is_same<T, float>::value, "MaxPoolingBackward is float only, as in the reference");
+  const std::string fn = "MaxPoolingBackward";
+  need_gpu(fn, "grad_output", grad_output.device);
+  need_gpu(fn, "mask", mask.device);
+  need_gpu(fn, "grad_input", grad_input.device);
+  if (kernel_shape.size() < 2) throw std::invalid_argument(fn + ": kernel_shape must end with [kh, kw]");
+  if (input_shape.size() < 2) throw std::invalid_argument(fn + ": input_shape must end with [H, W]");
+  const ConvShape go = conv_shape(fn, "grad_output", grad_output.shape);
+  const int H = input_shape[input_shape.size() - 2], W = input_shape.back();
+  const int kh = kernel_shape[kernel_shape.size() - 2], kw = kernel_shape.back();
+  if (conv_out(fn, H, kh, pad_h, stride_h) != go.H || conv_out(fn, W, kw, pad_w, stride_w) != go.W)
+    throw std::invalid_argument(fn + ": grad_output's last two axes do not match input_shape and the window");
+  if (mask.size != grad_output.size) throw std::invalid_argument(fn + ": mask must have grad_output's shape");
+  no_alias(fn, {{grad_output.p_data, "grad_output"}, {mask.p_data, "mask"}}, {{grad_input.p_data, "grad_input"}});
+  // the reference's shape: grad_output's leading axes, then H, W (Layers.cu:301-315)
+  std::vector<int> ishape(grad_output.shape.begin(), grad_output.shape.end() - 2);
+  ishape.insert(ishape.end(), {H, W});
+  grad_input.resize(ishape);
+  tt_check(tt_maxpool_backward_f32(grad_output.p_data, mask.p_data, grad_input.p_data, go.batch * go.C, H, W, kh, kw,
+                                   pad_h, pad_w, stride_h, stride_w, nullptr),
+           fn.c_str());
+  tt_check(tt_sync(), fn.c_str());
+}
+
 template void AttentionForward<float>(const TinyTensor<float>&, const TinyTensor<float>&, const TinyTensor<float>&,
                                       TinyTensor<float>&, TinyTensor<float>&, float, bool);
 template void AttentionForward<bf16>(const TinyTensor<bf16>&, const TinyTensor<bf16>&, const TinyTensor<bf16>&,
@@ -568,3 +619,7 @@ template void ConvBackward<bf16>(const TinyTensor<bf16>&, const TinyTensor<bf16>
 template float SoftmaxLoss<float>(const TinyTensor<float>&, const TinyTensor<int>&);
 template void CrossEntropyLoss<float>(const TinyTensor<float>&, const TinyTensor<int>&, TinyTensor<float>&);
 template void CrossEntropyLossBackward<float>(const TinyTensor<float>&, const TinyTensor<int>&, TinyTensor<float>&);
+template void MaxPoolingForward<float>(const TinyTensor<float>&, TinyTensor<float>&, TinyTensor<float>&,
+                                       const std::vector<int>&, int, int, int, int);
+template void MaxPoolingBackward<float>(const TinyTensor<float>&, const TinyTensor<float>&, TinyTensor<float>&,
+                                        const std::vector<int>&, const std::vector<int>&, int, int, int, int);

@@ -97,3 +97,16 @@ template <typename T>
 void CrossEntropyLossBackward(const TinyTensor<T>& softmax_output, const TinyTensor<int>& labels,
                               TinyTensor<T>& grad_input);
 
+// Max pooling (Layers.cu:254-322), float as the reference binds it: input
+// [.., C, H, W] -> output and mask [.., C, OH, OW] (mask: the flat index of
+// each window's first maximum in its plane); the backward routes grad_output
+// to those elements of a grad_input of input_shape, summing where windows
+// overlap.
+template <typename T>
+void MaxPoolingForward(const TinyTensor<T>& input, TinyTensor<T>& output, TinyTensor<T>& mask,
+                       const std::vector<int>& kernel_shape, int pad_h, int pad_w, int stride_h, int stride_w);
+template <typename T>
+void MaxPoolingBackward(const TinyTensor<T>& grad_output, const TinyTensor<T>& mask, TinyTensor<T>& grad_input,
+                        const std::vector<int>& input_shape, const std::vector<int>& kernel_shape, int pad_h,
+                        int pad_w, int stride_h, int stride_w);
+

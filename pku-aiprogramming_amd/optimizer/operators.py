@@ -30,7 +30,8 @@ gradients (the reference's wraps its arguments in new leaves, :432-433), and
 GEMM through ``myLayer.FcForward`` / ``FcBackward`` and ``Conv`` (:535-569)
 through ``myLayer.ConvForward`` / ``ConvBackward`` (im2col + the GEMM), and the
 softmax losses (:604-665) through ``myLayer.SoftmaxForward`` and the
-cross-entropy kernels; MaxPool (:570-602) is not part of this build.
+cross-entropy kernels, and ``MaxPool`` (:570-602) through
+``myLayer.MaxPoolingForward`` / ``MaxPoolingBackward``.
 """
 from __future__ import annotations
 
@@ -499,6 +500,49 @@ class Conv(TensorOp):
 
 def conv(input, weight, pad_h=0, pad_w=0, stride_h=1, stride_w=1):
     return Conv(pad_h, pad_w, stride_h, stride_w)(input, weight)
+
+
+class MaxPool(TensorOp):
+    """Max pooling over the last two axes on the GPU (reference :570-602):
+    the window's first largest element passes; its gradient goes back to that
+    element (summed where windows overlap).  Each output node keeps its own
+    device mask until its gradient is taken."""
+
+    def __init__(self, kernel_shape=(2, 2), pad_h=0, pad_w=0, stride_h=2, stride_w=2):
+        self.kernel_shape = [int(k) for k in kernel_shape]
+        self.pad_h, self.pad_w, self.stride_h, self.stride_w = pad_h, pad_w, stride_h, stride_w
+
+    def _args(self):
+        return self.kernel_shape, self.pad_h, self.pad_w, self.stride_h, self.stride_w
+
+    def _run(self, x):
+        xd = FC._dev(x)
+        out, mask = Tensor_float([1], "gpu"), Tensor_float([1], "gpu")
+        ml.MaxPoolingForward(xd, out, mask, *self._args())
+        return out, mask, list(np.shape(x))
+
+    def compute(self, input):
+        return self._run(input)[0].numpy()
+
+    def forward(self, node, input):
+        out, mask, shape = self._run(input)
+        node.saved = (mask, shape)
+        return out.numpy()
+
+    def gradient(self, out_grad, node):
+        saved = getattr(node, "saved", None)
+        if saved is None:
+            _, mask, shape = self._run(node.inputs[0].realize_cached_data())
+        else:
+            mask, shape = saved
+        node.saved = None
+        gx = Tensor_float([1], "gpu")
+        ml.MaxPoolingBackward(FC._dev(out_grad.realize_cached_data()), mask, gx, shape, *self._args())
+        return Tensor(gx, requires_grad=False)
+
+
+def maxpool(input, kernel_shape=(2, 2), pad_h=0, pad_w=0, stride_h=2, stride_w=2):
+    return MaxPool(kernel_shape, pad_h, pad_w, stride_h, stride_w)(input)
 
 
 def _labels_array(labels) -> np.ndarray:

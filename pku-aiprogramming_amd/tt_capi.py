@@ -60,6 +60,8 @@ _SIGS = {
     "tt_fill_normal": (C.c_int, [C.c_int, _p, _i64, C.c_uint64, C.c_float, _p]),
     "tt_im2col": (C.c_int, [C.c_int, _p, _p, _i64] + [C.c_int] * 10 + [_p]),
     "tt_cross_entropy_f32": (C.c_int, [_p, _p, _p, _i64, _i64, _p]),
+    "tt_maxpool_f32": (C.c_int, [_p, _p, _p, _i64] + [C.c_int] * 8 + [_p]),
+    "tt_maxpool_backward_f32": (C.c_int, [_p, _p, _p, _i64] + [C.c_int] * 8 + [_p]),
     "tt_cross_entropy_backward_f32": (C.c_int, [_p, _p, _p, _i64, _i64, _p]),
     "tt_col2im": (C.c_int, [C.c_int, _p, _p, _i64] + [C.c_int] * 10 + [_p]),
     "tt_attn_fwd_f32": (C.c_int, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, C.c_float, C.c_int, _p]),
